@@ -1,0 +1,63 @@
+"""Build recipe for libassocscan.so (gfx950), kept beside the package.
+
+The shared library is built in-tree (next to this file) so it travels with
+the source tree; nothing is installed into site-packages.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC_DIR = PKG_DIR.parent / "csrc"
+REPO_ROOT = PKG_DIR.parent.parent
+INCLUDE_DIR = REPO_ROOT / "include"
+LIB_NAME = "libassocscan.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+
+ARCH = os.environ.get("ASC_OFFLOAD_ARCH", "gfx950")
+
+# -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
+HIPCC_FLAGS = [
+  "-O3",
+  "-std=c++17",
+  "-fPIC",
+  "-shared",
+  f"--offload-arch={ARCH}",
+  "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+  "-Wall",
+]
+
+
+def hipcc() -> str:
+  path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+  if not Path(path).exists():
+    raise RuntimeError("hipcc not found; cannot build libassocscan")
+  return path
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None,
+          out: Path | None = None) -> Path:
+  """Compiles csrc/*.hip into one shared library and returns its path."""
+  out = Path(out) if out is not None else LIB_PATH
+  sources = sorted(str(p) for p in CSRC_DIR.glob("*.hip"))
+  tmp = out.with_name(out.name + f".tmp{os.getpid()}")
+  cmd = [hipcc(), *HIPCC_FLAGS, *(extra_flags or []), f"-I{INCLUDE_DIR}",
+         *sources, "-o", str(tmp)]
+  if verbose:
+    print(" ".join(cmd), flush=True)
+  res = subprocess.run(cmd, capture_output=True, text=True)
+  if res.returncode != 0:
+    raise RuntimeError(
+      f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+  if verbose and (res.stdout or res.stderr):
+    print(res.stdout, res.stderr, flush=True)
+  os.replace(tmp, out)
+  return out
+
+
+if __name__ == "__main__":
+  print(build(verbose=True))

@@ -1,0 +1,165 @@
+"""Tensor-level launchers over the libassocscan C ABI.
+
+Every public function of the package ends here.  These helpers validate
+shapes, dtypes, devices and contiguity on the host (no device sync), derive
+the geometry ``(num_seq, C, T)`` and launch on the current stream of the
+tensors' device.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from associative_scan_triton import _lib
+
+
+def _geometry(t: torch.Tensor, cu: torch.Tensor, num_channels: int | None
+              ) -> tuple[int, int, int]:
+  """Returns (num_seq, C, T) for a [C, T] (or flat [C*T]) tensor.
+
+  The reference reads the row stride from ``cu_seqlens[num_seq]`` on the
+  device (_kernels.py:51,108); here it is the tensor width, and callers must
+  keep ``cu_seqlens[-1] == T`` exactly as the reference requires.
+  """
+  if cu.dim() != 1 or cu.numel() < 1:
+    raise ValueError("cu_seqlens must be a 1-D tensor with num_seq + 1 entries")
+  num_seq = cu.numel() - 1
+  # Addressing is flat (row c starts at c*T), as in the reference kernels, so
+  # the channel count comes from the grid when given, else from the rows.
+  if num_channels is not None:
+    C = int(num_channels)
+  else:
+    C = t.shape[0] if t.dim() == 2 else 1
+  if C <= 0 or t.numel() % C:
+    raise ValueError(
+      f"a tensor of {t.numel()} elements cannot hold {C} channels")
+  return num_seq, C, t.numel() // C
+
+
+def _check_same(ref: torch.Tensor, *others: torch.Tensor | None) -> None:
+  for o in others:
+    if o is None:
+      continue
+    if o.dtype != ref.dtype:
+      raise TypeError(f"dtype mismatch: {ref.dtype} vs {o.dtype}")
+    if o.numel() != ref.numel():
+      raise ValueError(f"size mismatch: {tuple(ref.shape)} vs {tuple(o.shape)}")
+    if not o.is_contiguous():
+      raise ValueError("all scan tensors must be contiguous")
+  if not ref.is_contiguous():
+    raise ValueError("all scan tensors must be contiguous")
+
+
+class _OnDevice:
+  """Makes `dev` current for the duration of a launch."""
+
+  def __init__(self, dev: torch.device):
+    self.dev = dev
+    self.prev = None
+
+  def __enter__(self):
+    cur = torch.cuda.current_device()
+    if self.dev.index is not None and cur != self.dev.index:
+      self.prev = cur
+      torch.cuda.set_device(self.dev)
+    return self
+
+  def __exit__(self, *exc):
+    if self.prev is not None:
+      torch.cuda.set_device(self.prev)
+    return False
+
+
+def scan_fwd(gates: torch.Tensor, tokens: torch.Tensor, h_out: torch.Tensor,
+             cu: torch.Tensor, reverse: bool,
+             gate_prod_out: torch.Tensor | None = None,
+             num_channels: int | None = None) -> None:
+  """h_out <- scan(gates, tokens); optionally gate_prod_out <- prod(gates)."""
+  lib = _lib.load()
+  dev = _lib.require_device(gates, tokens, h_out, gate_prod_out, cu)
+  _check_same(tokens, gates, h_out, gate_prod_out)
+  dt = _lib.dtype_code(tokens)
+  cuc = _lib.cu_code(cu)
+  cu = cu.contiguous()
+  S, C, T = _geometry(tokens, cu, num_channels)
+  with _OnDevice(dev):
+    _lib.check(lib.asc_scan_fwd(
+      gates.data_ptr(), tokens.data_ptr(), h_out.data_ptr(),
+      _lib.ptr(gate_prod_out), cu.data_ptr(), cuc, S, C, T, dt,
+      1 if reverse else 0, _lib.stream_of(dev)))
+
+
+def scan_bwd(grad: torch.Tensor, gates: torch.Tensor, states: torch.Tensor,
+             d_tokens: torch.Tensor, d_gates: torch.Tensor, cu: torch.Tensor,
+             causal: bool, num_channels: int | None = None) -> None:
+  """Fused backward: (d_tokens, d_gates) of a scan given dy, g and h."""
+  lib = _lib.load()
+  dev = _lib.require_device(grad, gates, states, d_tokens, d_gates, cu)
+  _check_same(grad, gates, states, d_tokens, d_gates)
+  dt = _lib.dtype_code(grad)
+  cuc = _lib.cu_code(cu)
+  cu = cu.contiguous()
+  S, C, T = _geometry(grad, cu, num_channels)
+  with _OnDevice(dev):
+    _lib.check(lib.asc_scan_bwd(
+      grad.data_ptr(), gates.data_ptr(), states.data_ptr(),
+      d_tokens.data_ptr(), d_gates.data_ptr(), cu.data_ptr(), cuc, S, C, T,
+      dt, 1 if causal else 0, _lib.stream_of(dev)))
+
+
+def scan_bidi_fwd(gf: torch.Tensor, xf: torch.Tensor, gb: torch.Tensor,
+                  xb: torch.Tensor, hf: torch.Tensor, hb: torch.Tensor,
+                  cu: torch.Tensor, num_channels: int | None = None) -> None:
+  """Both bidirectional branches in one launch."""
+  lib = _lib.load()
+  dev = _lib.require_device(gf, xf, gb, xb, hf, hb, cu)
+  _check_same(xf, gf, gb, xb, hf, hb)
+  dt = _lib.dtype_code(xf)
+  cuc = _lib.cu_code(cu)
+  cu = cu.contiguous()
+  S, C, T = _geometry(xf, cu, num_channels)
+  with _OnDevice(dev):
+    _lib.check(lib.asc_scan_bidi_fwd(
+      gf.data_ptr(), xf.data_ptr(), gb.data_ptr(), xb.data_ptr(),
+      hf.data_ptr(), hb.data_ptr(), cu.data_ptr(), cuc, S, C, T, dt,
+      _lib.stream_of(dev)))
+
+
+def scan_bidi_bwd(dyf: torch.Tensor, dyb: torch.Tensor, gf: torch.Tensor,
+                  gb: torch.Tensor, hf: torch.Tensor, hb: torch.Tensor,
+                  dxf: torch.Tensor, dgf: torch.Tensor, dxb: torch.Tensor,
+                  dgb: torch.Tensor, cu: torch.Tensor,
+                  num_channels: int | None = None) -> None:
+  """Backward of both bidirectional branches in one launch."""
+  lib = _lib.load()
+  dev = _lib.require_device(dyf, dyb, gf, gb, hf, hb, dxf, dgf, dxb, dgb, cu)
+  _check_same(dyf, dyb, gf, gb, hf, hb, dxf, dgf, dxb, dgb)
+  dt = _lib.dtype_code(dyf)
+  cuc = _lib.cu_code(cu)
+  cu = cu.contiguous()
+  S, C, T = _geometry(dyf, cu, num_channels)
+  with _OnDevice(dev):
+    _lib.check(lib.asc_scan_bidi_bwd(
+      dyf.data_ptr(), dyb.data_ptr(), gf.data_ptr(), gb.data_ptr(),
+      hf.data_ptr(), hb.data_ptr(), dxf.data_ptr(), dgf.data_ptr(),
+      dxb.data_ptr(), dgb.data_ptr(), cu.data_ptr(), cuc, S, C, T, dt,
+      _lib.stream_of(dev)))
+
+
+def shift_pad(data: torch.Tensor, out: torch.Tensor, cu: torch.Tensor,
+              pad_value: float, backward: bool, wrap: bool) -> None:
+  """out <- segment-aware shift of a contiguous [C, L] tensor."""
+  lib = _lib.load()
+  dev = _lib.require_device(data, out, cu)
+  if data.dim() != 2:
+    raise ValueError(f"shift_pad expects a [C, BL] tensor, got {tuple(data.shape)}")
+  _check_same(data, out)
+  dt = _lib.dtype_code(data)
+  cuc = _lib.cu_code(cu)
+  cu = cu.contiguous()
+  C, L = data.shape
+  with _OnDevice(dev):
+    _lib.check(lib.asc_shift_pad(
+      data.data_ptr(), out.data_ptr(), cu.data_ptr(), cuc, cu.numel() - 1,
+      C, L, dt, float(pad_value), 1 if backward else 0, 1 if wrap else 0,
+      _lib.stream_of(dev)))

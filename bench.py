@@ -1,0 +1,269 @@
+"""Kernel-level benchmark of the chunked linear-recurrence scan on one MI355X.
+
+Default workload (the BASELINE metric's configuration, cfg5): causal scan,
+fp32, B=8 sequences of T=65536 packed along time, C=1536 channels
+(805,306,368 elements per tensor), chunk_size 128,
+g = 0.99 + 0.01*U(0,1), x ~ N(0,1), dy ~ U(0,1) (dense, as the reference's
+kernel bench uses rand_like, bench_kernels.py:296).  One "step" is one
+forward launch plus one fused backward launch over the whole batch, with all
+tensors resident in HBM (the reference's bench_kernels fwd+bwd subject,
+bench_kernels.py:279-312).
+
+Reported: whole-job algorithmic HBM throughput (GB/s) and ms per step;
+per-kernel average durations from HIP events recorded on the launch stream;
+the roofline of the dominant kernel (the backward, 20 B/element); the CPU
+baseline (the fp64-accumulating sequential oracle on the host cores, on a
+row sample of the same inputs); and a parity check of sampled rows against
+the oracle, outside the timed region.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg5]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "associative-scan-triton_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = ("fwd+bwd scan ms + achieved HBM GB/s (% peak), "
+          "B=8 C=1536 T=64K fp32")
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+
+# name -> (description, B, C, T, dtype, kind, gate range)
+CONFIGS = {
+  "cfg5": ("causal fwd+bwd, B=8 C=1536 T=65536, fp32, chunk 128, "
+           "g~0.99+0.01U(0,1)", 8, 1536, 65536, "float32", "causal", (0.99, 1.0)),
+  "cfg4": ("bidirectional fwd+bwd (both branches, one launch each way), "
+           "B=8 C=1536 T=16384, fp32, g~U(0.9,1)", 8, 1536, 16384, "float32",
+           "bidi", (0.9, 1.0)),
+  "cfg2": ("causal forward only, B=8 C=1536 T=4096, fp32, g=sigmoid(N(0,1))",
+           8, 1536, 4096, "float32", "fwd", None),
+  "cfg3": ("varlen causal fwd+bwd, 64 seqs U[16,8192], C=1024, bf16 storage, "
+           "fp32 accumulate, g~U(0.5,1)", 64, 1024, None, "bfloat16", "causal",
+           (0.5, 1.0)),
+}
+
+
+def log(*a):
+  print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+  p = argparse.ArgumentParser()
+  p.add_argument("--gpus", type=int, default=1)
+  p.add_argument("--steps", type=int, default=20)
+  p.add_argument("--warmup", type=int, default=5)
+  p.add_argument("--config", default="cfg5", choices=sorted(CONFIGS))
+  p.add_argument("--no-cpu-baseline", action="store_true")
+  p.add_argument("--no-check", action="store_true")
+  p.add_argument("--profile-copy", action="store_true",
+                 help="also launch one plain device copy of one tensor "
+                      "(rocprof byte-counter calibration)")
+  return p.parse_args()
+
+
+def main():
+  a = parse()
+  if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+    print(json.dumps({"error": "this build measures one GPU only; the scan "
+                      "shards over channels/sequences with no communication "
+                      "(see DESIGN.md); run with --gpus 1"}))
+    sys.exit(2)
+
+  import numpy as np
+  import torch
+
+  from associative_scan_triton import _ops
+
+  dev = torch.device("cuda:0")
+  desc, B, C, T, dts, kind, grange = CONFIGS[a.config]
+  dtype = getattr(torch, dts)
+  esize = torch.tensor([], dtype=dtype).element_size()
+
+  # ---- inputs (seeded, on the device) ----
+  gen = torch.Generator(device=dev).manual_seed(1155)
+  if T is None:  # varlen
+    lens = torch.randint(16, 8192 + 1, (B,),
+                         generator=torch.Generator().manual_seed(1155))
+    cu = torch.cat([torch.zeros(1, dtype=torch.int64), lens.cumsum(0)])
+    Tt = int(cu[-1])
+  else:
+    cu = torch.arange(B + 1, dtype=torch.int64) * T
+    Tt = B * T
+  cu = cu.to(torch.int32).to(dev)
+  N = C * Tt
+
+  def gates():
+    if grange is None:
+      return torch.randn(C, Tt, device=dev, generator=gen).sigmoid_().to(dtype)
+    lo, hi = grange
+    return torch.rand(C, Tt, device=dev, generator=gen).mul_(hi - lo).add_(lo).to(dtype)
+
+  def normal():
+    return torch.randn(C, Tt, device=dev, generator=gen).to(dtype)
+
+  nbr = 2 if kind == "bidi" else 1
+  g = [gates() for _ in range(nbr)]
+  x = [normal() for _ in range(nbr)]
+  h = [torch.empty_like(x[0]) for _ in range(nbr)]
+  with_bwd = kind != "fwd"
+  if with_bwd:
+    dy = [torch.rand(C, Tt, device=dev, generator=gen).to(dtype) for _ in range(nbr)]
+    dx = [torch.empty_like(x[0]) for _ in range(nbr)]
+    dg = [torch.empty_like(x[0]) for _ in range(nbr)]
+  torch.cuda.synchronize()
+  log(f"[bench] {a.config}: {desc}; N={N} elements/tensor, "
+      f"{torch.cuda.get_device_name(0)}")
+
+  def fwd():
+    if kind == "bidi":
+      _ops.scan_bidi_fwd(g[0], x[0], g[1], x[1], h[0], h[1], cu)
+    else:
+      _ops.scan_fwd(g[0], x[0], h[0], cu, reverse=False)
+
+  def bwd():
+    if kind == "bidi":
+      _ops.scan_bidi_bwd(dy[0], dy[1], g[0], g[1], h[0], h[1], dx[0], dg[0],
+                         dx[1], dg[1], cu)
+    else:
+      _ops.scan_bwd(dy[0], g[0], h[0], dx[0], dg[0], cu, causal=True)
+
+  if a.profile_copy:
+    tmp = torch.empty_like(x[0])
+    tmp.copy_(x[0])
+    torch.cuda.synchronize()
+    del tmp
+
+  for _ in range(a.warmup):
+    fwd()
+    if with_bwd:
+      bwd()
+  torch.cuda.synchronize()
+
+  # ---- timed region: K steps; events on the launch stream ----
+  stream = torch.cuda.current_stream(dev)
+  ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        for _ in range(a.steps)]
+  torch.cuda.synchronize()
+  t0 = time.perf_counter()
+  for k in range(a.steps):
+    ev[k][0].record(stream)
+    fwd()
+    ev[k][1].record(stream)
+    if with_bwd:
+      bwd()
+    ev[k][2].record(stream)
+  torch.cuda.synchronize()
+  wall = time.perf_counter() - t0
+  fwd_ms = [e[0].elapsed_time(e[1]) for e in ev]
+  bwd_ms = [e[1].elapsed_time(e[2]) for e in ev] if with_bwd else [0.0]
+  step_ms = ev[0][0].elapsed_time(ev[-1][2]) / a.steps
+  log(f"[bench] timed {a.steps} steps in {wall:.3f} s wall; "
+      f"fwd {np.mean(fwd_ms):.4f} ms, bwd {np.mean(bwd_ms):.4f} ms")
+
+  fwd_bytes = 3 * esize * N * nbr
+  bwd_bytes = 5 * esize * N * nbr if with_bwd else 0
+  step_bytes = fwd_bytes + bwd_bytes
+  gbs = step_bytes / (step_ms * 1e-3) / 1e9
+  f_ms, b_ms = float(np.mean(fwd_ms)), float(np.mean(bwd_ms))
+  if with_bwd:
+    dom, dom_ms, dom_bytes = "bwd", b_ms, bwd_bytes
+  else:
+    dom, dom_ms, dom_bytes = "fwd", f_ms, fwd_bytes
+  achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+
+  # ---- parity of sampled rows (outside the timed region) ----
+  check = None
+  if not a.no_check:
+    from oracle import oracle
+    rows = sorted({0, C // 2, C - 1})
+    cu_np = cu.cpu().numpy().astype(np.int64)
+    errs = {}
+    for b in range(nbr):
+      rev = b == 1
+      gs = g[b][rows].double().cpu().numpy()
+      xs = x[b][rows].double().cpu().numpy()
+      href = oracle.scan_fwd(gs, xs, cu_np, rev)
+      hg = h[b][rows].double().cpu().numpy()
+      errs[f"h{b}"] = float(np.max(np.abs(hg - href) / (1e-5 + np.abs(href))))
+      if with_bwd:
+        dxr, dgr = oracle.scan_bwd(dy[b][rows].double().cpu().numpy(), gs, hg,
+                                   cu_np, causal=not rev)
+        errs[f"dx{b}"] = float(np.max(np.abs(dx[b][rows].double().cpu().numpy() - dxr)
+                                      / (1e-5 + np.abs(dxr))))
+        errs[f"dg{b}"] = float(np.max(np.abs(dg[b][rows].double().cpu().numpy() - dgr)
+                                      / (1e-5 + np.abs(dgr))))
+    check = {"rows": rows, "max_rel_err_vs_fp64_oracle": errs,
+             "criterion": "|got-ref| / (1e-5 + |ref|)"}
+    log(f"[bench] parity on rows {rows}: {errs}")
+
+  # ---- CPU baseline on a row sample of the same inputs ----
+  cpu = None
+  if not a.no_cpu_baseline and with_bwd and kind == "causal" and dtype == torch.float32:
+    from oracle import oracle
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rows = max(1, C // 4)
+    gs = g[0][:rows].cpu().numpy()
+    xs = x[0][:rows].cpu().numpy()
+    dys = dy[0][:rows].cpu().numpy()
+    outs = tuple(np.empty_like(xs) for _ in range(3))
+    cu_np = cu.cpu().numpy().astype(np.int64)
+    oracle.fwd_bwd_f32io(gs, xs, dys, cu_np, rows, threads, out=outs)  # page-in
+    t1 = time.perf_counter()
+    oracle.fwd_bwd_f32io(gs, xs, dys, cu_np, rows, threads, out=outs)
+    cpu_s = time.perf_counter() - t1
+    n_s = rows * Tt
+    cpu = {"value": round(32 * n_s / cpu_s / 1e9, 3), "unit": "GB/s",
+           "cores": threads, "kind": "port",
+           "sample": f"first {rows} of {C} channels, all {B} sequences "
+                     f"({n_s} elements, fwd+bwd, fp32 storage, fp64 "
+                     f"accumulation, OpenMP over (sequence, channel) rows); "
+                     f"{cpu_s:.3f} s",
+           "ms_per_step_equiv": round(cpu_s * 1e3 * N / n_s, 1)}
+    log(f"[bench] cpu baseline: {cpu}")
+
+  traffic = None
+  tf = ROOT / "profiles" / f"traffic_{a.config}.json"
+  if tf.exists():
+    traffic = json.loads(tf.read_text()).get(dom)
+
+  out = {
+    "metric": METRIC,
+    "value": round(gbs, 2),
+    "unit": "GB/s",
+    "n_gpus": 1,
+    "steps": a.steps,
+    "warmup": a.warmup,
+    "ms_per_step": round(step_ms, 4),
+    "higher_is_better": True,
+    "scaling": "weak",
+    "vs_baseline": None,
+    "dtype": {"float32": "f32", "bfloat16": "bf16"}[dts],
+    "data": "synthetic (seeded device RNG)",
+    "config": {"workload": f"{a.config}: {desc}", "B": B, "C": C,
+               "T": T, "elements_per_tensor": N, "chunk_size": 128},
+    "pct_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+    "elements_per_s": round(N * nbr / (step_ms * 1e-3), 1),
+    "fwd_ms": round(f_ms, 4),
+    "bwd_ms": round(b_ms, 4),
+    "fwd_gbs": round(fwd_bytes / (f_ms * 1e-3) / 1e9, 2),
+    "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 2),
+                 "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                 "frac": round(achieved / PEAK_HBM_GBS, 4),
+                 "traffic": traffic,
+                 "algorithmic_bytes": dom_bytes},
+    "cpu_baseline": cpu,
+    "check": check,
+  }
+  print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+  main()

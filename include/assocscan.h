@@ -1,0 +1,154 @@
+/*
+ * assocscan.h - C ABI of libassocscan, the MI355X (gfx950) chunked
+ * linear-recurrence scan  h[t] = g[t] * h[t-1] + x[t].
+ *
+ * Layout shared by every entry point: a tensor is C rows ("channels") of
+ * T = seq_stride elements each, time contiguous (element (c, t) lives at
+ * index c * T + t).  Packed variable-length sequences ("segments") are given
+ * by cu_seqlens[0..num_seq]: segment s of every row covers the time range
+ * [cu_seqlens[s], cu_seqlens[s+1]).  cu_seqlens lives in device memory and is
+ * read by the kernels; values are clamped to [0, T] on the device so that a
+ * malformed cu_seqlens can never make a kernel touch memory outside the
+ * tensors (it yields meaningless results instead).
+ *
+ * All pointers are device pointers.  Every call is asynchronous on `stream`
+ * (a hipStream_t; NULL = the legacy default stream).  The library never
+ * allocates, frees or synchronises.  Return value: 0 on success, a negative
+ * ASC_E_* code for an invalid argument (nothing is launched), or a positive
+ * hipError_t from the launch.  asc_strerror() turns any of them into text.
+ *
+ * The reference is the Triton package associative-scan-triton 1.0.0; the
+ * citations below name the reference function each entry point replaces.
+ */
+#ifndef ASSOCSCAN_H
+#define ASSOCSCAN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of the scanned tensors (accumulation is always fp32). */
+enum {
+  ASC_F32 = 0,
+  ASC_F16 = 1,
+  ASC_BF16 = 2
+};
+
+/* Element types of cu_seqlens. */
+enum {
+  ASC_CU_I32 = 0,
+  ASC_CU_I64 = 1
+};
+
+/* Negative status codes (positive codes are hipError_t values). */
+enum {
+  ASC_OK = 0,
+  ASC_E_NULL = -1,       /* a required pointer is NULL                     */
+  ASC_E_DTYPE = -2,      /* unknown dtype / cu dtype                      */
+  ASC_E_SIZE = -3,       /* negative or overflowing sizes                 */
+  ASC_E_ALIGN = -4,      /* a pointer is not aligned to its element size  */
+  ASC_E_ARG = -5         /* any other invalid argument                    */
+};
+
+/* ABI version of this header; bumped on any signature change. */
+#define ASC_ABI_VERSION 1
+int asc_abi_version(void);
+
+/* Human-readable text for a status code returned by any entry point. */
+const char* asc_strerror(int status);
+
+/*
+ * Forward scan over every (segment, channel) pair.
+ *   reverse = 0:  h[t] = g[t]*h[t-1] + x[t],  h[start]  = x[start]
+ *   reverse = 1:  h[t] = g[t]*h[t+1] + x[t],  h[end-1]  = x[end-1]
+ * gate_prod_out (nullable): also writes the running gate product
+ *   A[t] = prod g over [start..t] (reverse: over [t..end-1]).
+ * In-place use is allowed: h_out may equal tokens and gate_prod_out may
+ * equal gates (each element is read before it is overwritten).
+ *
+ * Replaces: _dispatcher.py:12-70 forward_scan_full, which launches
+ *   _kernels.py:19-81  forward_scan_chunked (one chunk) or
+ *   _kernels.py:84-168 forward_scan_onepass_pipelined (many chunks);
+ *   TESTING=True there corresponds to gate_prod_out = gates here and
+ *   INPLACE=True to h_out = tokens.
+ */
+int asc_scan_fwd(const void* gates, const void* tokens, void* h_out,
+                 void* gate_prod_out, const void* cu_seqlens, int cu_dtype,
+                 int64_t num_seq, int64_t num_channels, int64_t seq_stride,
+                 int dtype, int reverse, void* stream);
+
+/*
+ * Fused backward of a forward scan (reads dy, g, h once; writes dx, dg).
+ *   causal = 1 (backward of reverse=0):
+ *     dx[t] = dy[t] + g[t+1]*dx[t+1],  dx[end-1] = dy[end-1]
+ *     dg[t] = h[t-1]*dx[t],            h[start-1] := 0
+ *   causal = 0 (backward of reverse=1):
+ *     dx[t] = dy[t] + g[t-1]*dx[t-1],  dx[start] = dy[start]
+ *     dg[t] = h[t+1]*dx[t],            h[end] := 0
+ *
+ * Replaces: _dispatcher.py:73-117 backward_scan_fused_full, which launches
+ *   _kernels.py:171-287 backward_scan_fused or
+ *   _kernels.py:290-374 backward_scan_fused_single_chunk.
+ */
+int asc_scan_bwd(const void* grad, const void* gates, const void* states,
+                 void* d_tokens, void* d_gates, const void* cu_seqlens,
+                 int cu_dtype, int64_t num_seq, int64_t num_channels,
+                 int64_t seq_stride, int dtype, int causal, void* stream);
+
+/*
+ * Both branches of the bidirectional scan in ONE launch: a causal scan of
+ * (gates_fwd, tokens_fwd) into h_fwd and a reverse scan of
+ * (gates_bwd, tokens_bwd) into h_bwd.
+ *
+ * Replaces: scan_eager.py:122-131 (two forward_scan_full launches in
+ *   ScanBidirectionalBranched.forward) and scan_compiled.py:229-238.
+ */
+int asc_scan_bidi_fwd(const void* gates_fwd, const void* tokens_fwd,
+                      const void* gates_bwd, const void* tokens_bwd,
+                      void* h_fwd, void* h_bwd, const void* cu_seqlens,
+                      int cu_dtype, int64_t num_seq, int64_t num_channels,
+                      int64_t seq_stride, int dtype, void* stream);
+
+/*
+ * Backward of both bidirectional branches in ONE launch: causal backward of
+ * the forward branch and anti-causal backward of the reverse branch.
+ *
+ * Replaces: scan_eager.py:160-169 (two backward_scan_fused_full launches in
+ *   ScanBidirectionalBranched.backward) and scan_compiled.py:270-277.
+ */
+int asc_scan_bidi_bwd(const void* grad_fwd, const void* grad_bwd,
+                      const void* gates_fwd, const void* gates_bwd,
+                      const void* states_fwd, const void* states_bwd,
+                      void* d_tokens_fwd, void* d_gates_fwd,
+                      void* d_tokens_bwd, void* d_gates_bwd,
+                      const void* cu_seqlens, int cu_dtype, int64_t num_seq,
+                      int64_t num_channels, int64_t seq_stride, int dtype,
+                      void* stream);
+
+/*
+ * Segment-aware shift by one position with padding, on a contiguous
+ * [num_channels, seq_len] tensor.
+ *   backward = 1: out[:, p] = data[:, p-1], pad at every segment start
+ *                 (p = cu_seqlens[s], s < num_seq)
+ *   backward = 0: out[:, p] = data[:, p+1], pad at every segment end
+ *                 (p = cu_seqlens[s] - 1, s >= 1)
+ * Positions that are not a boundary read their neighbour; at the two row
+ * ends the neighbour index wraps around (wrap = 1, torch.roll semantics of
+ * the eager reference) or is clamped into the row (wrap = 0, the compiled
+ * reference kernel).  pad_value is rounded to the tensor dtype.
+ *
+ * Replaces: _shift_pad.py:18-55 shift_pad (wrap = 1) and
+ *   _shift_pad.py:63-165 _shift_pad_kernel / shift_pad_compiled (wrap = 0).
+ */
+int asc_shift_pad(const void* data, void* out, const void* cu_seqlens,
+                  int cu_dtype, int64_t num_seq, int64_t num_channels,
+                  int64_t seq_len, int dtype, double pad_value, int backward,
+                  int wrap, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ASSOCSCAN_H */

@@ -1,0 +1,75 @@
+"""C ABI surface of the built library (CPU only: no kernel is launched).
+
+The library must load, report its ABI version, and export every entry point
+that include/assocscan.h declares.  Argument validation happens on the host
+before any HIP call, so invalid calls can be exercised without a GPU.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from associative_scan_triton import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "assocscan.h"
+
+
+def _declared():
+  text = HEADER.read_text()
+  text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+  return sorted(set(re.findall(r"\b(asc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_is_built():
+  assert _lib.LIB_PATH.exists(), "run __graft_entry__.build() first"
+
+
+def test_exports_every_declared_symbol():
+  lib = ctypes.CDLL(str(_lib.LIB_PATH))
+  names = _declared()
+  assert names, "no declarations parsed"
+  missing = [n for n in names if not hasattr(lib, n)]
+  assert not missing, f"declared but not exported: {missing}"
+  # and the ctypes binding covers exactly the declared set
+  assert sorted(_lib.SIGNATURES) == names
+
+
+def test_abi_version_and_strerror():
+  lib = _lib.load()
+  assert lib.asc_abi_version() == 1
+  assert lib.asc_strerror(0) == b"success"
+  for code in (-1, -2, -3, -4, -5):
+    assert lib.asc_strerror(code) and lib.asc_strerror(code) != b"unknown error"
+  assert lib.asc_strerror(-99) == b"unknown error"
+
+
+def _fwd(lib, **kw):
+  a = dict(gates=8, tokens=8, h_out=8, gate_prod_out=None, cu=8, cu_dtype=0,
+           S=1, C=1, T=4, dtype=0, reverse=0, stream=None)
+  a.update(kw)
+  return lib.asc_scan_fwd(*a.values())
+
+
+def test_host_validation_codes():
+  lib = _lib.load()
+  assert _fwd(lib, gates=None) == -1
+  assert _fwd(lib, cu=None) == -1
+  assert _fwd(lib, dtype=7) == -2
+  assert _fwd(lib, cu_dtype=3) == -2
+  assert _fwd(lib, S=-1) == -3
+  assert _fwd(lib, C=-2) == -3
+  assert _fwd(lib, tokens=6) == -4          # fp32 pointer not 4-byte aligned
+  assert _fwd(lib, cu=10, cu_dtype=1) == -4  # int64 cu not 8-byte aligned
+  # empty problems are a successful no-op (nothing is launched)
+  assert _fwd(lib, S=0) == 0
+  assert _fwd(lib, C=0) == 0
+  assert lib.asc_scan_bwd(8, 8, 8, 8, None, 8, 0, 1, 1, 4, 0, 1, None) == -1
+  assert lib.asc_shift_pad(8, 8, 8, 0, 1, 1, 4, 5, 0.0, 1, 1, None) == -2
+
+
+def test_error_is_raised_with_message():
+  with pytest.raises(_lib.AscError, match="NULL"):
+    _lib.check(-1)

@@ -1,0 +1,554 @@
+"""GPU parity tests: the gfx950 kernels (through the C ABI, via the public
+API) against the fp64 oracle and the reference's known-answer vectors.
+
+Inputs are generated on the CPU with seeded torch generators, so the oracle
+and the kernels see identical values.  Tolerances (elementwise
+|got - ref| <= atol + rtol*|ref|) are in tests/_helpers.py: fp32 rtol 1e-5.
+"""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import associative_scan_triton as ast
+from _helpers import (DEV, TOL, check_close, cu_of, grid_args, make, npf,
+                      oracle_bwd, oracle_fwd)
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+GOLD = json.loads(
+  (Path(__file__).parent / "golden" / "known_answers.json").read_text())
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+DT_IDS = ["f32", "f16", "bf16"]
+
+# Segment-length sets: single elements, lengths around the 16-byte vector
+# and the 64-vector sub-tile (256 fp32 / 512 half elements), odd lengths,
+# and a few thousand.
+LENS = [
+  [1],
+  [3],
+  [4],
+  [1, 1, 1, 1, 1],
+  [255],
+  [256],
+  [257],
+  [511, 512, 513],
+  [1000, 3, 4097],
+  [17, 1, 2, 3, 1024, 1025, 250],
+  [2 * 4096 + 3, 7],
+]
+
+
+# ---------------------------------------------------------------------------
+# known-answer vectors (reference tests)
+# ---------------------------------------------------------------------------
+
+def _gold_tensors(case):
+  g = torch.tensor(case["g"], dtype=torch.float32, device=DEV)
+  x = torch.tensor(case["x"], dtype=torch.float32, device=DEV)
+  cu = torch.tensor(case["cu"], device=DEV)
+  return g, x, cu
+
+
+@pytest.mark.parametrize("case", GOLD["forward"], ids=lambda c: c["name"])
+def test_golden_forward_scan_full(case):
+  """forward_scan_full in place with TESTING=True (gates <- A)."""
+  for chunk in case["chunk_sizes"]:
+    g, x, cu = _gold_tensors(case)
+    cu_np = np.array(case["cu"])
+    grid = ast.get_grid(len(cu_np), int(np.diff(cu_np).max()), chunk,
+                        case["channels"])
+    ast.forward_scan_full(g, x, cu, grid, REVERSE=case["reverse"],
+                          CHUNK_SIZE=chunk, TESTING=True)
+    exp_h = torch.tensor(case["h"], device=DEV).reshape(x.shape)
+    assert torch.allclose(x, exp_h, rtol=case["rtol"], atol=case["atol"]), x
+    if "A" in case:
+      exp_a = torch.tensor(case["A"], device=DEV).reshape(g.shape)
+      assert torch.allclose(g, exp_a, rtol=case["rtol"], atol=case["atol"]), g
+
+
+@pytest.mark.parametrize("case", GOLD["forward"], ids=lambda c: c["name"])
+def test_golden_kernel_objects(case):
+  """kernel[grid](...) call convention (test_scan_kernels.py:160-168)."""
+  g, x, cu = _gold_tensors(case)
+  chunk = case["chunk_sizes"][0]
+  cu_np = np.array(case["cu"])
+  grid = ast.get_grid(len(cu_np), int(np.diff(cu_np).max()), chunk,
+                      case["channels"])
+  out = torch.empty_like(x)
+  ast.forward_scan_chunked[grid](
+    gates_ptr=g, tokens_ptr=x, tokens_out_ptr=out, cu_seqlens_ptr=cu,
+    REVERSE=case["reverse"], CHUNK_SIZE=chunk, TESTING=False, INPLACE=False)
+  exp_h = torch.tensor(case["h"], device=DEV).reshape(x.shape)
+  assert torch.allclose(out, exp_h, rtol=case["rtol"], atol=case["atol"])
+  out2 = torch.empty_like(x)
+  ast.forward_scan_onepass_pipelined[(grid[0], grid[2])](
+    gates_ptr=g, tokens_ptr=x, tokens_out_ptr=out2, cu_seqlens_ptr=cu,
+    REVERSE=case["reverse"], CHUNK_SIZE=chunk, NUM_CHUNKS=grid[1],
+    TESTING=False, NUM_STAGES=3, INPLACE=False)
+  assert torch.equal(out, out2)
+  # inputs untouched when TESTING=False and INPLACE=False
+  g0, x0, _ = _gold_tensors(case)
+  assert torch.equal(g, g0) and torch.equal(x, x0)
+
+
+@pytest.mark.parametrize("case", GOLD["causal_grad"], ids=lambda c: c["name"])
+@pytest.mark.parametrize("compiled", [False, True])
+def test_golden_causal_grad(case, compiled):
+  """test_scan_causal.py:19-71, eager and compiled."""
+  fn = ast.scan_causal_compiled if compiled else ast.scan_causal
+  for chunk in case["chunk_sizes"]:
+    g = torch.tensor([case["g"]], device=DEV, requires_grad=True)
+    x = torch.tensor([case["x"]], device=DEV, requires_grad=True)
+    cu = torch.tensor(case["cu"], device=DEV)
+    grid = ast.get_grid(len(case["cu"]), 4, chunk, 1)
+    y = fn(g, x, {"cu_seqlens": cu, "chunk_size": chunk, "grid": grid})
+    tol = dict(rtol=case["rtol"], atol=case["atol"])
+    assert torch.allclose(y, torch.tensor([case["h"]], device=DEV), **tol)
+    y.sum().backward()
+    assert torch.allclose(g.grad, torch.tensor([case["dg"]], device=DEV), **tol)
+    assert torch.allclose(x.grad, torch.tensor([case["dx"]], device=DEV), **tol)
+
+
+# ---------------------------------------------------------------------------
+# random parity against the fp64 oracle
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("reverse", [False, True], ids=["causal", "reverse"])
+@pytest.mark.parametrize("lens", LENS, ids=lambda l: "x".join(map(str, l))[:40])
+def test_forward_parity(dtype, reverse, lens):
+  C = 3
+  g, x = make(lens, C, dtype)
+  gd, xd = g.to(DEV), x.to(DEV)
+  h = torch.empty_like(xd)
+  a = torch.empty_like(gd)
+  cu = torch.tensor(cu_of(lens), device=DEV, dtype=torch.int32)
+  from associative_scan_triton import _ops
+  _ops.scan_fwd(gd, xd, h, cu, reverse=reverse, gate_prod_out=a)
+  ref, a_ref = oracle.scan_fwd(npf(g), npf(x), cu_of(lens), reverse,
+                               gate_prod=True)
+  check_close(h, ref, dtype, "h")
+  check_close(a, a_ref, dtype, "gate product")
+  assert torch.equal(gd, g.to(DEV)) and torch.equal(xd, x.to(DEV))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "anticausal"])
+@pytest.mark.parametrize("lens", LENS, ids=lambda l: "x".join(map(str, l))[:40])
+def test_backward_parity(dtype, causal, lens):
+  C = 3
+  g, h, dy = make(lens, C, dtype, n=3)
+  dx = torch.empty(C, sum(lens), dtype=dtype, device=DEV)
+  dg = torch.empty_like(dx)
+  cu = torch.tensor(cu_of(lens), device=DEV, dtype=torch.int64)
+  from associative_scan_triton import _ops
+  _ops.scan_bwd(dy.to(DEV), g.to(DEV), h.to(DEV), dx, dg, cu, causal=causal)
+  dx_ref, dg_ref = oracle.scan_bwd(npf(dy), npf(g), npf(h), cu_of(lens), causal)
+  check_close(dx, dx_ref, dtype, "dx")
+  check_close(dg, dg_ref, dtype, "dg")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("lens", [[37], [1, 600, 2], [4096, 4096]],
+                         ids=lambda l: "x".join(map(str, l)))
+def test_scan_causal_autograd_parity(dtype, lens):
+  C = 4
+  g, x, dy = make(lens, C, dtype, n=3)
+  args = grid_args(lens, C)
+  gd = g.to(DEV).requires_grad_(True)
+  xd = x.to(DEV).requires_grad_(True)
+  y = ast.scan_causal(gd, xd, args)
+  y.backward(dy.to(DEV))
+  h_ref = oracle_fwd(g, x, lens)
+  check_close(y, h_ref, dtype, "h")
+  dx_ref, dg_ref = oracle_bwd(dy, g, npf(y), lens)
+  check_close(xd.grad, dx_ref, dtype, "dx")
+  check_close(gd.grad, dg_ref, dtype, "dg")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("compiled", [False, True], ids=["eager", "compiled"])
+@pytest.mark.parametrize("lens", [[5], [64, 1, 300], [2048, 33]],
+                         ids=lambda l: "x".join(map(str, l)))
+def test_bidirectional_parity(dtype, compiled, lens):
+  C = 3
+  gf, xf, dyf = make(lens, C, dtype, seed=1, glo=0.9, n=3)
+  gb, xb, dyb = make(lens, C, dtype, seed=2, glo=0.9, n=3)
+  args = grid_args(lens, C)
+  fn = (ast.scan_bidirectional_branched_compiled if compiled
+        else ast.scan_bidirectional_branched)
+  ts = [t.to(DEV).requires_grad_(True) for t in (gf, xf, gb, xb)]
+  yf, yb = fn(*ts, args)
+  torch.autograd.backward([yf, yb], [dyf.to(DEV), dyb.to(DEV)])
+  hf = oracle_fwd(gf, xf, lens)
+  hb = oracle_fwd(gb, xb, lens, reverse=True)
+  check_close(yf, hf, dtype, "h fwd branch")
+  check_close(yb, hb, dtype, "h bwd branch")
+  dxf, dgf = oracle_bwd(dyf, gf, npf(yf), lens, causal=True)
+  dxb, dgb = oracle_bwd(dyb, gb, npf(yb), lens, causal=False)
+  check_close(ts[0].grad, dgf, dtype, "dg fwd")
+  check_close(ts[1].grad, dxf, dtype, "dx fwd")
+  check_close(ts[2].grad, dgb, dtype, "dg bwd")
+  check_close(ts[3].grad, dxb, dtype, "dx bwd")
+
+
+def test_bidirectional_compiled_matches_eager():
+  """test_compiled.py:49-89 (B in {1,4}, T in {64,256}, C=64, chunk 128)."""
+  for B in (1, 4):
+    for T in (64, 256):
+      lens = [T] * B
+      gen = torch.Generator().manual_seed(1155)
+      C = 64
+      gf, gb = torch.rand(C, T * B, generator=gen), torch.rand(C, T * B, generator=gen)
+      xf, xb = torch.randn(C, T * B, generator=gen), torch.randn(C, T * B, generator=gen)
+      args = grid_args(lens, C)
+      d = [t.to(DEV) for t in (gf, xf, gb, xb)]
+      ref = ast.scan_bidirectional_branched(*[t.clone() for t in d], args)
+      got = ast.scan_bidirectional_branched_compiled(*[t.clone() for t in d], args)
+      torch.testing.assert_close(ref[0], got[0], rtol=1e-5, atol=1e-5)
+      torch.testing.assert_close(ref[1], got[1], rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# segment boundaries: exact, and no leakage across documents
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+def test_segment_boundaries_bit_exact(dtype):
+  lens = [1, 2, 3, 257, 64, 1, 513, 9]
+  C = 5
+  g, x, dy = make(lens, C, dtype, n=3, glo=-2.0, ghi=2.0)
+  # signed zeros and a zero at segment heads
+  x[:, 0] = -0.0
+  x[1, 3] = -0.0
+  dy[:, -1] = -0.0
+  cu = cu_of(lens)
+  heads, tails = cu[:-1], cu[1:] - 1
+  cud = torch.tensor(cu, device=DEV)
+  from associative_scan_triton import _ops
+  gd, xd, dyd = g.to(DEV), x.to(DEV), dy.to(DEV)
+  for rev in (False, True):
+    h = torch.empty_like(xd)
+    _ops.scan_fwd(gd, xd, h, cud, reverse=rev)
+    first = tails if rev else heads
+    got = h[:, first].cpu()
+    assert torch.equal(got.view(torch.int16 if dtype != torch.float32 else torch.int32),
+                       x[:, first].view(torch.int16 if dtype != torch.float32 else torch.int32))
+    dx = torch.empty_like(xd)
+    dg = torch.empty_like(xd)
+    _ops.scan_bwd(dyd, gd, h, dx, dg, cud, causal=not rev)
+    start = heads if rev else tails        # first element of the adjoint scan
+    last = tails if rev else heads         # where the shifted state is padded
+    iv = torch.int16 if dtype != torch.float32 else torch.int32
+    assert torch.equal(dx[:, start].cpu().view(iv), dy[:, start].view(iv))
+    exp = (torch.zeros((), dtype=torch.float32) * dx[:, last].float()).to(dtype)
+    assert torch.equal(dg[:, last].cpu().view(iv), exp.cpu().view(iv))
+
+
+def test_nonfinite_values_stay_in_their_segment():
+  lens = [300, 5, 700, 1]
+  C = 2
+  g, x, dy = make(lens, C, n=3)
+  cu = cu_of(lens)
+  g[:, cu[1] + 2] = float("inf")
+  x[:, cu[1] + 1] = float("nan")
+  dy[:, cu[1] + 3] = float("nan")
+  gd, xd = g.to(DEV), x.to(DEV)
+  from associative_scan_triton import _ops
+  cud = torch.tensor(cu, device=DEV)
+  for rev in (False, True):
+    h = torch.empty_like(xd)
+    _ops.scan_fwd(gd, xd, h, cud, reverse=rev)
+    dx = torch.empty_like(xd)
+    dg = torch.empty_like(xd)
+    _ops.scan_bwd(dy.to(DEV), gd, h, dx, dg, cud, causal=not rev)
+    ref = oracle.scan_fwd(npf(g), npf(x), cu, rev)
+    ok = np.r_[0:cu[1], cu[2]:cu[4]]
+    check_close(h[:, ok], ref[:, ok], torch.float32, "h outside the bad segment")
+    dxr, dgr = oracle.scan_bwd(npf(dy), npf(g), npf(h), cu, not rev)
+    check_close(dx[:, ok], dxr[:, ok], torch.float32, "dx outside")
+    check_close(dg[:, ok], dgr[:, ok], torch.float32, "dg outside")
+
+
+# ---------------------------------------------------------------------------
+# layouts: flat 1-D tensors, misaligned views, int32/int64 cu_seqlens
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("offsets", [(1, 1, 1), (2, 2, 2), (3, 1, 2), (0, 1, 0)],
+                         ids=["phase1", "phase2", "mixed", "mixed2"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_misaligned_views(offsets, dtype):
+  lens = [700, 1, 33, 1500]
+  C = 3
+  T = sum(lens)
+  g, x, dy = make(lens, C, dtype, n=3)
+
+  def view_at(src, off):
+    buf = torch.zeros(C * T + 16, dtype=dtype, device=DEV)
+    v = buf[off:off + C * T].view(C, T)
+    v.copy_(src.to(DEV))
+    return v
+
+  gd, xd = view_at(g, offsets[0]), view_at(x, offsets[1])
+  h = view_at(torch.zeros_like(x), offsets[2])
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  from associative_scan_triton import _ops
+  _ops.scan_fwd(gd, xd, h, cu, reverse=False)
+  check_close(h, oracle_fwd(g, x, lens), dtype, "h (misaligned)")
+  dx = view_at(torch.zeros_like(x), offsets[0])
+  dg = view_at(torch.zeros_like(x), offsets[2])
+  _ops.scan_bwd(view_at(dy, offsets[1]), gd, h, dx, dg, cu, causal=True)
+  dxr, dgr = oracle.scan_bwd(npf(dy), npf(g), npf(h), cu_of(lens), True)
+  check_close(dx, dxr, dtype, "dx (misaligned)")
+  check_close(dg, dgr, dtype, "dg (misaligned)")
+
+
+def test_flat_layout_and_cu_dtypes():
+  """1-D [C*T] tensors addressed with the grid's channel count, as the
+  reference's test data (test_utils.py:89-100)."""
+  lens = [3, 5, 8]
+  C = 2
+  g, x = make(lens, C)
+  ref = oracle_fwd(g, x, lens)
+  for cu_dtype in (torch.int32, torch.int64):
+    cu = torch.tensor(cu_of(lens), device=DEV, dtype=cu_dtype)
+    grid = ast.get_grid(len(cu), 8, 4, C)
+    gd, xd = g.flatten().to(DEV), x.flatten().to(DEV)
+    ast.forward_scan_full(gd, xd, cu, grid, REVERSE=False, CHUNK_SIZE=4,
+                          TESTING=False)
+    check_close(xd.view(C, -1), ref, torch.float32, f"flat h {cu_dtype}")
+
+
+# ---------------------------------------------------------------------------
+# reference dtype tests (test_scan_dtypes.py)
+# ---------------------------------------------------------------------------
+
+REF_TOL = {  # test_scan_dtypes.py:42-46
+  torch.float32: {"atol": 1e-5, "rtol": 1e-4},
+  torch.float16: {"atol": 5e-3, "rtol": 5e-2},
+  torch.bfloat16: {"atol": 3e-2, "rtol": 1e-1},
+}
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("seqlen", [32, 128, 512, 1024])
+@pytest.mark.parametrize("num_channels", [1, 4])
+def test_reference_forward_vs_gold(dtype, seqlen, num_channels):
+  """test_scan_dtypes.py:62-90 with inputs drawn on the CPU."""
+  gen = torch.Generator().manual_seed(1155)
+  g = torch.rand(num_channels, seqlen, generator=gen).to(dtype)
+  x = torch.randn(num_channels, seqlen, generator=gen).to(dtype)
+  chunk = min(seqlen, 512)
+  args = grid_args([seqlen], num_channels, chunk)
+  y = ast.scan_causal(g.to(DEV), x.to(DEV), args)
+  gold = torch.from_numpy(oracle_fwd(g, x, [seqlen]))
+  torch.testing.assert_close(y.cpu().double(), gold, **REF_TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_reference_multi_chunk_rmse(dtype):
+  """test_scan_dtypes.py:115-142: fp16 RMSE < 1e-3, bf16 < 5e-3."""
+  gen = torch.Generator().manual_seed(1155)
+  g = torch.rand(4, 1024, generator=gen).to(dtype)
+  x = torch.randn(4, 1024, generator=gen).to(dtype)
+  y = ast.scan_causal(g.to(DEV), x.to(DEV), grid_args([1024], 4, 512))
+  rmse = float(np.sqrt(np.mean((npf(y) - oracle_fwd(g, x, [1024])) ** 2)))
+  assert rmse < (1e-3 if dtype == torch.float16 else 5e-3), rmse
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+def test_reference_varlen_packed(dtype):
+  """test_scan_dtypes.py:221-256."""
+  seqlens = [32, 64, 128]
+  gen = torch.Generator().manual_seed(1155)
+  g = torch.rand(2, 224, generator=gen).to(dtype)
+  x = torch.randn(2, 224, generator=gen).to(dtype)
+  y = ast.scan_causal(g.to(DEV), x.to(DEV), grid_args(seqlens, 2, 128))
+  ref = oracle_fwd(g, x, seqlens)
+  torch.testing.assert_close(y.cpu().double(), torch.from_numpy(ref),
+                             **REF_TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("seqlen", [64, 256, 1024])
+def test_reference_bidi_vs_gold(dtype, seqlen):
+  """test_scan_dtypes.py:148-189 (reverse gold = flip o scan o flip)."""
+  gen = torch.Generator().manual_seed(1155)
+  ts = [torch.rand(4, seqlen, generator=gen).to(dtype) if i % 2 == 0
+        else torch.randn(4, seqlen, generator=gen).to(dtype) for i in range(4)]
+  yf, yb = ast.scan_bidirectional_branched(
+    *[t.to(DEV) for t in ts], grid_args([seqlen], 4, min(seqlen, 512)))
+  gold_f = oracle_fwd(ts[0], ts[1], [seqlen])
+  gold_b = oracle.scan_fwd(npf(ts[2])[:, ::-1], npf(ts[3])[:, ::-1],
+                           [0, seqlen])[:, ::-1]
+  torch.testing.assert_close(yf.cpu().double(), torch.from_numpy(gold_f),
+                             **REF_TOL[dtype])
+  torch.testing.assert_close(yb.cpu().double(),
+                             torch.from_numpy(np.ascontiguousarray(gold_b)),
+                             **REF_TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("seqlen", [64, 512, 1024])
+def test_reference_bidi_backward_finite(dtype, seqlen):
+  """test_scan_dtypes.py:191-215."""
+  ts = [(torch.rand if i % 2 == 0 else torch.randn)(4, seqlen, dtype=dtype,
+                                                     device=DEV).requires_grad_(True)
+        for i in range(4)]
+  yf, yb = ast.scan_bidirectional_branched(*ts, grid_args([seqlen], 4, 512))
+  (yf.sum() + yb.sum()).backward()
+  for t in ts:
+    assert t.grad is not None and torch.isfinite(t.grad).all()
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+def test_accuracy_no_worse_than_reference(dtype):
+  """RMSE against the fp64 gold at C=4, T in {128, 512, 2048, 8192}
+  (bench_accuracy.py:31-37) must not exceed the reference's published RMSE
+  (README.md:266-281) by more than sampling noise (inputs differ: the
+  reference drew them with the CUDA generator).  Averaged over 4 seeds."""
+  acc = GOLD["accuracy_rmse"]
+  key = {torch.float32: "fp32", torch.float16: "fp16", torch.bfloat16: "bf16"}[dtype]
+  for T, pub in zip(acc["seqlens"], acc[key]):
+    rmses = []
+    for seed in range(4):
+      gen = torch.Generator().manual_seed(42 + seed)
+      g = torch.rand(4, T, generator=gen).to(dtype)
+      x = torch.randn(4, T, generator=gen).to(dtype)
+      y = ast.scan_causal(g.to(DEV), x.to(DEV), grid_args([T], 4, min(T, 512)))
+      rmses.append(np.sqrt(np.mean((npf(y) - oracle_fwd(g, x, [T])) ** 2)))
+    assert np.mean(rmses) <= 1.25 * pub, (key, T, np.mean(rmses), pub)
+
+
+# ---------------------------------------------------------------------------
+# shift_pad
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", GOLD["shift_pad"]["cases"], ids=lambda c: c["name"])
+@pytest.mark.parametrize("backward", [True, False])
+def test_shift_pad_golden(case, backward):
+  pad = GOLD["shift_pad"]["pad"]
+  data = torch.tensor(case["data"], device=DEV)
+  cu = torch.tensor(case["cu"], device=DEV)
+  exp = torch.tensor(case["backward" if backward else "forward"], device=DEV)
+  assert torch.equal(ast.shift_pad(data, cu, pad, backward), exp)
+  assert torch.equal(ast.shift_pad_compiled(data, cu, pad, backward), exp)
+
+
+def test_shift_pad_zero_length_raises():
+  z = GOLD["shift_pad"]["zero_length"]
+  with pytest.raises(AssertionError, match=z["message"]):
+    ast.shift_pad(torch.tensor(z["data"], device=DEV),
+                  torch.tensor(z["cu"], device=DEV), -1, True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("backward", [True, False])
+@pytest.mark.parametrize("pad_value", [0.0, 1.0, -1.5])
+def test_shift_pad_parity(dtype, backward, pad_value):
+  """Random data vs the oracle; compiled == eager bit for bit
+  (test_compiled.py:91-104)."""
+  gen = torch.Generator().manual_seed(9)
+  lens = [64, 1, 700, 3, 1300]
+  C, L = 7, sum(lens)
+  data = torch.randn(C, L, generator=gen).to(dtype)
+  cu = torch.tensor(cu_of(lens), device=DEV, dtype=torch.int32)
+  dd = data.to(DEV)
+  eager = ast.shift_pad(dd, cu, pad_value, backward)
+  comp = ast.shift_pad_compiled(dd, cu, pad_value, backward)
+  assert torch.equal(eager, comp)
+  ref = oracle.shift_pad(npf(data), cu_of(lens), pad_value, backward, wrap=True)
+  ref_t = torch.from_numpy(ref).to(dtype)
+  assert torch.equal(eager.cpu(), ref_t)
+
+
+# ---------------------------------------------------------------------------
+# torch.compile / custom-op checks
+# ---------------------------------------------------------------------------
+
+def test_custom_ops_opcheck():
+  lens = [40, 9]
+  C = 3
+  g, x, dy = make(lens, C, n=3)
+  cu = torch.tensor(cu_of(lens), device=DEV, dtype=torch.int32)
+  gd = g.to(DEV).requires_grad_(True)
+  xd = x.to(DEV).requires_grad_(True)
+  torch.library.opcheck(torch.ops.associative_scan_triton.scan_causal_fwd,
+                        (gd, xd, cu, 1, C, 64))
+  torch.library.opcheck(torch.ops.associative_scan_triton.scan_bidi_fwd,
+                        (gd, xd, gd, xd, cu, 1, C, 64))
+  torch.library.opcheck(torch.ops.associative_scan_triton.shift_pad,
+                        (xd.detach(), cu, 0.0, True))
+
+
+def test_torch_compile_fullgraph():
+  lens = [100, 28]
+  C = 4
+  g, x = make(lens, C)
+  args = grid_args(lens, C)
+
+  def f(g, x):
+    return ast.scan_causal_compiled(g, x, args).square().sum()
+
+  cf = torch.compile(f, backend="aot_eager", fullgraph=True)
+  gd = g.to(DEV).requires_grad_(True)
+  xd = x.to(DEV).requires_grad_(True)
+  loss = cf(gd, xd)
+  loss.backward()
+  g2 = g.to(DEV).requires_grad_(True)
+  x2 = x.to(DEV).requires_grad_(True)
+  loss2 = f(g2, x2)
+  loss2.backward()
+  torch.testing.assert_close(loss, loss2)
+  torch.testing.assert_close(gd.grad, g2.grad)
+  torch.testing.assert_close(xd.grad, x2.grad)
+
+
+def test_backward_kernel_objects():
+  """backward_scan_fused[grid](...) as bench_kernels.py:119-135 calls it."""
+  lens = [1024, 1024]
+  C = 2
+  g, h, dy = make(lens, C, n=3)
+  cu = torch.tensor(cu_of(lens), device=DEV, dtype=torch.int32)
+  grid = ast.get_grid(3, 1024, 128, C)
+  outs = []
+  for kern, gr in ((ast.backward_scan_fused, (grid[0], grid[2])),
+                   (ast.backward_scan_fused_single_chunk, (grid[0], 1, grid[2]))):
+    dx = torch.empty(C, 2048, device=DEV)
+    dg = torch.empty_like(dx)
+    kw = dict(grad_ptr=dy.to(DEV), gates_ptr=g.to(DEV), states_ptr=h.to(DEV),
+              d_tokens_ptr=dx, d_gates_ptr=dg, cu_seqlens_ptr=cu,
+              CHUNK_SIZE=128, CAUSAL=True)
+    if kern is ast.backward_scan_fused:
+      kw.update(NUM_CHUNKS=grid[1], NUM_STAGES=3)
+    kern[gr](**kw)
+    outs.append((dx, dg))
+  dxr, dgr = oracle.scan_bwd(npf(dy), npf(g), npf(h), cu_of(lens), True)
+  for dx, dg in outs:
+    check_close(dx, dxr, torch.float32, "dx")
+    check_close(dg, dgr, torch.float32, "dg")
+  dxb = torch.empty(C, 2048, device=DEV)
+  dgb = torch.empty_like(dxb)
+  ast.backward_scan_fused_full(dy.to(DEV), g.to(DEV), h.to(DEV), dxb, dgb, cu,
+                               grid, CHUNK_SIZE=128, CAUSAL=True)
+  assert torch.equal(dxb, outs[0][0]) and torch.equal(dgb, outs[0][1])
+
+
+def test_stream_semantics():
+  """Launches go to the caller's current stream."""
+  lens = [5000]
+  g, x = make(lens, 8)
+  gd, xd = g.to(DEV), x.to(DEV)
+  s = torch.cuda.Stream()
+  with torch.cuda.stream(s):
+    h = torch.empty_like(xd)
+    from associative_scan_triton import _ops
+    _ops.scan_fwd(gd, xd, h, torch.tensor(cu_of(lens), device=DEV), False)
+  s.synchronize()
+  check_close(h, oracle_fwd(g, x, lens), torch.float32, "h on side stream")

@@ -1,0 +1,132 @@
+"""Full-size configurations (the BASELINE configs) on one MI355X.
+
+Each test runs the kernels on the whole tensor, then checks a sample of
+rows against the fp64 oracle (every segment of those rows, full length) and
+size-independent properties on the whole tensor (exact segment heads, no
+non-finite values).  Inputs are drawn on the device with a seeded generator;
+the sampled rows are copied back and given to the oracle unchanged.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import DEV, check_close, npf
+from associative_scan_triton import _ops
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(seed):
+  return torch.Generator(device=DEV).manual_seed(seed)
+
+
+def _rows(C):
+  return sorted({0, 1, C // 2, C - 1})
+
+
+def _check_fwd_bwd(g, x, dy, h, dx, dg, cu, dtype, rows, reverse=False):
+  cu_np = cu.cpu().numpy().astype(np.int64)
+  gs, xs, dys = npf(g[rows]), npf(x[rows]), npf(dy[rows])
+  h_ref = oracle.scan_fwd(gs, xs, cu_np, reverse)
+  check_close(h[rows], h_ref, dtype, "h (sampled rows)")
+  dx_ref, dg_ref = oracle.scan_bwd(dys, gs, npf(h[rows]), cu_np,
+                                   causal=not reverse)
+  scale = max(1.0, float(np.abs(dx_ref).max()) * 1e-2)
+  check_close(dx[rows], dx_ref, dtype, "dx (sampled rows)", scale)
+  check_close(dg[rows], dg_ref, dtype, "dg (sampled rows)", scale)
+  # whole tensor: exact heads, all finite
+  heads = cu[1:].long() - 1 if reverse else cu[:-1].long()
+  assert torch.equal(h[:, heads], x[:, heads])
+  for t in (h, dx, dg):
+    assert torch.isfinite(t).all()
+
+
+def test_cfg5_long_causal_fp32_fwd_bwd():
+  """B=8, C=1536, T=65536, fp32, g ~ 0.99 + 0.01 U(0,1) (805M elements)."""
+  C, B, T = 1536, 8, 65536
+  gen = _gen(5)
+  g = torch.rand(C, B * T, device=DEV, generator=gen).mul_(0.01).add_(0.99)
+  x = torch.randn(C, B * T, device=DEV, generator=gen)
+  dy = torch.rand(C, B * T, device=DEV, generator=gen)
+  cu = torch.arange(B + 1, device=DEV, dtype=torch.int32) * T
+  h, dx, dg = torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)
+  _ops.scan_fwd(g, x, h, cu, reverse=False)
+  _ops.scan_bwd(dy, g, h, dx, dg, cu, causal=True)
+  torch.cuda.synchronize()
+  _check_fwd_bwd(g, x, dy, h, dx, dg, cu, torch.float32, _rows(C))
+
+
+def test_cfg2_forward_fp32():
+  """B=8, C=1536, T=4096, fp32, g = sigmoid(N(0,1)); forward only."""
+  C, B, T = 1536, 8, 4096
+  gen = _gen(2)
+  g = torch.randn(C, B * T, device=DEV, generator=gen).sigmoid_()
+  x = torch.randn(C, B * T, device=DEV, generator=gen)
+  cu = torch.arange(B + 1, device=DEV, dtype=torch.int32) * T
+  h = torch.empty_like(x)
+  _ops.scan_fwd(g, x, h, cu, reverse=False)
+  rows = list(range(0, C, 97))
+  ref = oracle.scan_fwd(npf(g[rows]), npf(x[rows]),
+                        cu.cpu().numpy().astype(np.int64))
+  check_close(h[rows], ref, torch.float32, "h")
+  assert torch.equal(h[:, cu[:-1].long()], x[:, cu[:-1].long()])
+
+
+def test_cfg3_varlen_bf16_fwd_bwd():
+  """64 packed sequences, lengths U[16, 8192], C=1024, bf16 storage."""
+  C = 1024
+  lens = torch.randint(16, 8192 + 1, (64,), generator=torch.Generator().manual_seed(1155))
+  cu = torch.cat([torch.zeros(1, dtype=torch.int64), lens.cumsum(0)]).to(DEV)
+  Tt = int(lens.sum())
+  gen = _gen(3)
+  g = (0.5 + 0.5 * torch.rand(C, Tt, device=DEV, generator=gen)).bfloat16()
+  x = torch.randn(C, Tt, device=DEV, generator=gen).bfloat16()
+  dy = torch.randn(C, Tt, device=DEV, generator=gen).bfloat16()
+  h, dx, dg = torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)
+  _ops.scan_fwd(g, x, h, cu, reverse=False)
+  _ops.scan_bwd(dy, g, h, dx, dg, cu, causal=True)
+  torch.cuda.synchronize()
+  _check_fwd_bwd(g, x, dy, h, dx, dg, cu, torch.bfloat16, _rows(C))
+
+
+def test_cfg4_bidi_fp32_fwd_bwd():
+  """B=8, C=1536, T=16384, both branches, gates ~ U(0.9, 1)."""
+  C, B, T = 1536, 8, 16384
+  gen = _gen(4)
+  mk = lambda: torch.rand(C, B * T, device=DEV, generator=gen).mul_(0.1).add_(0.9)  # noqa: E731
+  gf, gb = mk(), mk()
+  xf = torch.randn(C, B * T, device=DEV, generator=gen)
+  xb = torch.randn(C, B * T, device=DEV, generator=gen)
+  dyf = torch.randn(C, B * T, device=DEV, generator=gen)
+  dyb = torch.randn(C, B * T, device=DEV, generator=gen)
+  cu = torch.arange(B + 1, device=DEV, dtype=torch.int32) * T
+  hf, hb = torch.empty_like(xf), torch.empty_like(xb)
+  _ops.scan_bidi_fwd(gf, xf, gb, xb, hf, hb, cu)
+  outs = [torch.empty_like(xf) for _ in range(4)]
+  _ops.scan_bidi_bwd(dyf, dyb, gf, gb, hf, hb, *outs, cu)
+  torch.cuda.synchronize()
+  rows = _rows(C)
+  _check_fwd_bwd(gf, xf, dyf, hf, outs[0], outs[1], cu, torch.float32, rows)
+  _check_fwd_bwd(gb, xb, dyb, hb, outs[2], outs[3], cu, torch.float32, rows,
+                 reverse=True)
+
+
+def test_cfg1_small_causal():
+  """C=4, one sequence T=128, chunk 128, g ~ U(0,1), x ~ N(0,1)."""
+  import associative_scan_triton as ast
+  gen = torch.Generator().manual_seed(1155)
+  g = torch.rand(4, 128, generator=gen)
+  x = torch.randn(4, 128, generator=gen)
+  cu = torch.tensor([0, 128], dtype=torch.int32, device=DEV)
+  args = {"cu_seqlens": cu, "chunk_size": 128, "grid": ast.get_grid(2, 128, 128, 4)}
+  gd = g.to(DEV).requires_grad_(True)
+  xd = x.to(DEV).requires_grad_(True)
+  y = ast.scan_causal(gd, xd, args)
+  y.sum().backward()
+  h_ref = oracle.scan_fwd(npf(g), npf(x), [0, 128])
+  dx_ref, dg_ref = oracle.scan_bwd(np.ones((4, 128)), npf(g), npf(y), [0, 128])
+  check_close(y, h_ref, torch.float32, "h")
+  check_close(xd.grad, dx_ref, torch.float32, "dx")
+  check_close(gd.grad, dg_ref, torch.float32, "dg")
