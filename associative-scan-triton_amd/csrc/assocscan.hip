@@ -41,11 +41,23 @@
 #ifndef ASC_BWD_UNROLL
 #define ASC_BWD_UNROLL 2
 #endif
+// Sub-tiles per wave and iteration of the workgroup-cooperative kernels.
+#ifndef ASC_WG_UNROLL
+#define ASC_WG_UNROLL 1
+#endif
+// Non-temporal (streaming) hints on the 16-byte loads / stores.
+#ifndef ASC_NT_LOAD
+#define ASC_NT_LOAD 1
+#endif
+#ifndef ASC_NT_STORE
+#define ASC_NT_STORE 1
+#endif
 
 namespace {
 
 constexpr int kWave = 64;
 constexpr int kWPB = ASC_WAVES_PER_BLOCK;
+constexpr int kUW = ASC_WG_UNROLL;
 
 // ---------------------------------------------------------------------------
 // Storage types.  V elements per 16-byte vector; ES bytes per element.
@@ -113,6 +125,22 @@ struct IoHalf {
 };
 using IoF16 = IoHalf<h2f, f2h>;
 using IoBF16 = IoHalf<b2f, f2b>;
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline uint4 ld16(const char* p) {
+  const u32x4* q = reinterpret_cast<const u32x4*>(p);
+  const u32x4 v = ASC_NT_LOAD ? __builtin_nontemporal_load(q) : *q;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ inline void st16(char* p, uint4 v) {
+  u32x4* q = reinterpret_cast<u32x4*>(p);
+  const u32x4 w = {v.x, v.y, v.z, v.w};
+  if (ASC_NT_STORE)
+    __builtin_nontemporal_store(w, q);
+  else
+    *q = w;
+}
 
 // ---------------------------------------------------------------------------
 // Cross-lane primitives (DPP).  update_dpp leaves `old` in lanes whose source
@@ -213,6 +241,19 @@ __device__ constexpr int mem_idx(int i) {
   return REV ? V - 1 - i : i;
 }
 
+// Byte offset of the lane's vector from the lowest-addressed vector of its
+// sub-tile (lane 0 comes first in scan order).
+template <bool REV>
+__device__ inline uint32_t lane_off(int lane) {
+  return static_cast<uint32_t>(REV ? (kWave - 1 - lane) : lane) * 16u;
+}
+
+// Lowest-addressed vector of sub-tile k.
+template <class IO, bool REV>
+__device__ inline int64_t sub_lo(const Walk<IO, REV>& w, int64_t k) {
+  return REV ? w.v1 - k * kWave - (kWave - 1) : w.v0 + k * kWave;
+}
+
 // Loads one vector of `origin` for the given lane into f[] (memory order).
 // MASKED: elements outside [P0, P1) (or an invalid lane) read `ident`.
 template <class IO, bool ALN, bool MASKED>
@@ -223,7 +264,7 @@ __device__ inline void load_vec(const char* origin, int64_t vi, bool lane_ok,
   const int64_t pv = vi * V;
   if (!MASKED) {
     if (ALN) {
-      IO::unpack(*reinterpret_cast<const uint4*>(origin + vi * 16), f);
+      IO::unpack(ld16(origin + vi * 16), f);
     } else {
 #pragma unroll
       for (int j = 0; j < V; ++j) f[j] = IO::load1(origin + (pv + j) * IO::ES);
@@ -232,7 +273,7 @@ __device__ inline void load_vec(const char* origin, int64_t vi, bool lane_ok,
   }
   const bool full = lane_ok && pv >= P0 && pv + V <= P1;
   if (ALN && full) {
-    IO::unpack(*reinterpret_cast<const uint4*>(origin + vi * 16), f);
+    IO::unpack(ld16(origin + vi * 16), f);
     return;
   }
 #pragma unroll
@@ -252,7 +293,7 @@ __device__ inline void store_vec(char* origin, int64_t vi, bool lane_ok,
   const int64_t pv = vi * V;
   if (!MASKED) {
     if (ALN) {
-      *reinterpret_cast<uint4*>(origin + vi * 16) = IO::pack(f);
+      st16(origin + vi * 16, IO::pack(f));
     } else {
 #pragma unroll
       for (int j = 0; j < V; ++j) IO::store1(origin + (pv + j) * IO::ES, f[j]);
@@ -261,7 +302,7 @@ __device__ inline void store_vec(char* origin, int64_t vi, bool lane_ok,
   }
   const bool full = lane_ok && pv >= P0 && pv + V <= P1;
   if (ALN && full) {
-    *reinterpret_cast<uint4*>(origin + vi * 16) = IO::pack(f);
+    st16(origin + vi * 16, IO::pack(f));
     return;
   }
 #pragma unroll
@@ -281,14 +322,19 @@ struct FwdPtrs {
   char* a;        // gate-product output origin, or nullptr
 };
 
-// One sub-tile: g, x in memory order (already masked to the identity when
-// MASKED); writes h (and the gate product when WA) in memory order.
-template <class IO, bool REV, bool MASKED, bool WA>
-__device__ inline void fwd_subtile(const float* g, const float* x, int64_t pv,
-                                   int64_t phead, float& carry, float& carry_a,
-                                   float* hout, float* aout) {
+// First phase of a sub-tile: the lane's exclusive prefix map (ea, ex) and
+// the sub-tile's total map (ta, tx, uniform across the wave).
+struct SubScan {
+  float ea, ex, ta, tx;
+};
+
+// Lane-serial scan of the lane's elements, then the 64-lane DPP scan.
+// g, x in memory order (masked to the identity when MASKED); phead is the
+// segment's first element in scan order (reset exactly there).
+template <class IO, bool REV, bool MASKED>
+__device__ inline SubScan fwd_local(const float* g, const float* x, int64_t pv,
+                                    int64_t phead) {
   constexpr int V = IO::V;
-  // 1. serial scan of the lane's own elements -> lane map (A, X)
   float A = 1.0f, X = 0.0f;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
@@ -304,14 +350,23 @@ __device__ inline void fwd_subtile(const float* g, const float* x, int64_t pv,
       A = A * g[j];
     }
   }
-  // 2. wave scan of lane maps; 3. exclusive prefix applied to the carry
   wave_scan_affine(A, X);
-  const float ta = readlane(A, kWave - 1);
-  const float tx = readlane(X, kWave - 1);
-  const float ea = dpp<kWaveShr1, 0xf>(1.0f, A);
-  const float ex = dpp<kWaveShr1, 0xf>(0.0f, X);
-  float hh = fmaf(ea, carry, ex);
-  // 4. re-walk
+  SubScan r;
+  r.ta = readlane(A, kWave - 1);
+  r.tx = readlane(X, kWave - 1);
+  r.ea = dpp<kWaveShr1, 0xf>(1.0f, A);
+  r.ex = dpp<kWaveShr1, 0xf>(0.0f, X);
+  return r;
+}
+
+// Second phase: the lane re-walks its elements from its prefix applied to
+// the carry into the sub-tile; h in memory order.
+template <class IO, bool REV, bool MASKED>
+__device__ inline void fwd_apply(const float* g, const float* x, int64_t pv,
+                                 int64_t phead, const SubScan& s, float carry,
+                                 float* hout) {
+  constexpr int V = IO::V;
+  float hh = fmaf(s.ea, carry, s.ex);
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int j = mem_idx<V, REV>(i);
@@ -321,7 +376,18 @@ __device__ inline void fwd_subtile(const float* g, const float* x, int64_t pv,
       hh = fmaf(g[j], hh, x[j]);
     hout[j] = hh;
   }
-  carry = fmaf(ta, carry, tx);
+}
+
+// One sub-tile with a carry in a register; writes h (and the gate product
+// when WA) in memory order.
+template <class IO, bool REV, bool MASKED, bool WA>
+__device__ inline void fwd_subtile(const float* g, const float* x, int64_t pv,
+                                   int64_t phead, float& carry, float& carry_a,
+                                   float* hout, float* aout) {
+  constexpr int V = IO::V;
+  const SubScan s = fwd_local<IO, REV, MASKED>(g, x, pv, phead);
+  fwd_apply<IO, REV, MASKED>(g, x, pv, phead, s, carry, hout);
+  carry = fmaf(s.ta, carry, s.tx);
   if (WA) {
     float p = 1.0f;
 #pragma unroll
@@ -364,6 +430,57 @@ __device__ inline void fwd_block(const FwdPtrs& t, const Walk<IO, REV>& w,
   }
 }
 
+// Interior sub-tiles [k, kend) ((kend - k) a positive multiple of U), all
+// full and aligned.  Software-pipelined: the loads of the next block of U
+// sub-tiles are issued before the current block is scanned, so each wave
+// keeps 2*U*16 bytes per lane and tensor in flight while it computes.
+template <class IO, bool REV, bool WA, int U>
+__device__ inline void fwd_fast(const FwdPtrs& t, const Walk<IO, REV>& w,
+                                int64_t k, int64_t kend, int lane,
+                                float& carry, float& carry_a) {
+  constexpr int V = IO::V;
+  constexpr int STEP = REV ? -kWave * 16 : kWave * 16;  // bytes per sub-tile
+  const uint32_t lo = lane_off<REV>(lane);
+  uint4 ga[U], xa[U], gb[U], xb[U];
+  auto load = [&](uint4(&g)[U], uint4(&x)[U], int64_t kk) {
+    const int64_t b = sub_lo(w, kk) * 16;
+    const char* gp = t.g + b + lo;
+    const char* xp = t.x + b + lo;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      g[u] = ld16(gp + u * STEP);
+      x[u] = ld16(xp + u * STEP);
+    }
+  };
+  auto run = [&](const uint4(&g)[U], const uint4(&x)[U], int64_t kk) {
+    const int64_t b = sub_lo(w, kk) * 16;
+    char* hp = t.h + b + lo;
+    char* ap = WA ? t.a + b + lo : nullptr;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float gf[V], xf[V], hf[V], af[V];
+      IO::unpack(g[u], gf);
+      IO::unpack(x[u], xf);
+      fwd_subtile<IO, REV, false, WA>(gf, xf, 0, 0, carry, carry_a, hf, af);
+      st16(hp + u * STEP, IO::pack(hf));
+      if (WA) st16(ap + u * STEP, IO::pack(af));
+    }
+  };
+  load(ga, xa, k);
+  while (true) {
+    const bool more = k + U < kend;
+    if (more) load(gb, xb, k + U);
+    run(ga, xa, k);
+    k += U;
+    if (!more) break;
+    const bool more2 = k + U < kend;
+    if (more2) load(ga, xa, k + U);
+    run(gb, xb, k);
+    k += U;
+    if (!more2) break;
+  }
+}
+
 template <class IO, bool REV, bool ALN, bool WA>
 __device__ void fwd_item(const FwdPtrs& t, int64_t P0, int64_t P1, int lane) {
   constexpr int U = ASC_FWD_UNROLL;
@@ -371,8 +488,16 @@ __device__ void fwd_item(const FwdPtrs& t, int64_t P0, int64_t P1, int lane) {
   float carry = 0.0f, carry_a = 1.0f;
   fwd_block<IO, REV, ALN, WA, true, 1>(t, w, 0, lane, carry, carry_a);
   int64_t k = 1;
-  for (; k + U <= w.kfast; k += U)
-    fwd_block<IO, REV, ALN, WA, false, U>(t, w, k, lane, carry, carry_a);
+  if (ALN) {
+    const int64_t nfull = (w.kfast - 1) / U * U;
+    if (nfull > 0) {
+      fwd_fast<IO, REV, WA, U>(t, w, 1, 1 + nfull, lane, carry, carry_a);
+      k = 1 + nfull;
+    }
+  } else {
+    for (; k + U <= w.kfast; k += U)
+      fwd_block<IO, REV, ALN, WA, false, U>(t, w, k, lane, carry, carry_a);
+  }
   for (; k < w.kfast; ++k)
     fwd_block<IO, REV, ALN, WA, false, 1>(t, w, k, lane, carry, carry_a);
   for (; k < w.nsub; ++k)
@@ -394,6 +519,70 @@ struct BwdPtrs {
   char* dg;
 };
 
+// First phase of a backward sub-tile.  carry_g is the gate of the element
+// just before the sub-tile in B order (it shifts into lane 0); returns the
+// lane's shifted gate for its first element in gprev.
+template <class IO, bool RB, bool MASKED>
+__device__ inline SubScan bwd_local(const float* g, const float* dy, int64_t pv,
+                                    int64_t phead, float carry_g,
+                                    float& gprev) {
+  constexpr int V = IO::V;
+  constexpr int jl = mem_idx<V, RB>(V - 1);  // last element in B order
+  gprev = dpp<kWaveShr1, 0xf>(carry_g, g[jl]);
+  float A = 1.0f, X = 0.0f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int j = mem_idx<V, RB>(i);
+    const float gs = (i == 0) ? gprev : g[mem_idx<V, RB>(i - 1)];
+    if (MASKED && pv + j == phead) {
+      A = 0.0f;
+      X = dy[j];
+    } else if (i == 0 && !MASKED) {
+      A = gs;
+      X = dy[j];
+    } else {
+      X = fmaf(gs, X, dy[j]);
+      A = A * gs;
+    }
+  }
+  wave_scan_affine(A, X);
+  SubScan r;
+  r.ta = readlane(A, kWave - 1);
+  r.tx = readlane(X, kWave - 1);
+  r.ea = dpp<kWaveShr1, 0xf>(1.0f, A);
+  r.ex = dpp<kWaveShr1, 0xf>(0.0f, X);
+  return r;
+}
+
+// Second phase: dx by re-walking from the prefix, dg = shifted state * dx.
+// hnext_in is the state of the element just after the sub-tile in B order
+// (it shifts into lane 63); ptail is the segment's last element in B order,
+// whose shifted state is the pad 0.
+template <class IO, bool RB, bool MASKED>
+__device__ inline void bwd_apply(const float* g, const float* dy,
+                                 const float* h, int64_t pv, int64_t phead,
+                                 int64_t ptail, float gprev, float hnext_in,
+                                 const SubScan& s, float carry, float* dxo,
+                                 float* dgo) {
+  constexpr int V = IO::V;
+  constexpr int jf = mem_idx<V, RB>(0);  // first element in B order
+  const float hnx = dpp<kWaveShl1, 0xf>(hnext_in, h[jf]);
+  float d = fmaf(s.ea, carry, s.ex);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int j = mem_idx<V, RB>(i);
+    const float gs = (i == 0) ? gprev : g[mem_idx<V, RB>(i - 1)];
+    if (MASKED && pv + j == phead)
+      d = dy[j];
+    else
+      d = fmaf(gs, d, dy[j]);
+    float hn = (i == V - 1) ? hnx : h[mem_idx<V, RB>(i + 1)];
+    if (MASKED && pv + j == ptail) hn = 0.0f;
+    dxo[j] = d;
+    dgo[j] = hn * d;
+  }
+}
+
 template <class IO, bool RB, bool MASKED>
 __device__ inline void bwd_subtile(const float* g, const float* dy,
                                    const float* h, int64_t pv, int64_t phead,
@@ -401,51 +590,12 @@ __device__ inline void bwd_subtile(const float* g, const float* dy,
                                    float& carry_g, float hnext_in,
                                    float* dxo, float* dgo) {
   constexpr int V = IO::V;
-  constexpr int jl = mem_idx<V, RB>(V - 1);  // last element in B order
-  constexpr int jf = mem_idx<V, RB>(0);      // first element in B order
-  // shifted gate for the lane's first element: previous lane's last gate
-  const float gprev = dpp<kWaveShr1, 0xf>(carry_g, g[jl]);
-  // shifted state for the lane's last element: next lane's first state
-  const float hnx = dpp<kWaveShl1, 0xf>(hnext_in, h[jf]);
-  float gs[V];
-#pragma unroll
-  for (int i = 0; i < V; ++i)
-    gs[i] = (i == 0) ? gprev : g[mem_idx<V, RB>(i - 1)];
-  float A = 1.0f, X = 0.0f;
-#pragma unroll
-  for (int i = 0; i < V; ++i) {
-    const int j = mem_idx<V, RB>(i);
-    if (MASKED && pv + j == phead) {
-      A = 0.0f;
-      X = dy[j];
-    } else if (i == 0 && !MASKED) {
-      A = gs[0];
-      X = dy[j];
-    } else {
-      X = fmaf(gs[i], X, dy[j]);
-      A = A * gs[i];
-    }
-  }
-  wave_scan_affine(A, X);
-  const float ta = readlane(A, kWave - 1);
-  const float tx = readlane(X, kWave - 1);
-  const float ea = dpp<kWaveShr1, 0xf>(1.0f, A);
-  const float ex = dpp<kWaveShr1, 0xf>(0.0f, X);
-  float d = fmaf(ea, carry, ex);
-#pragma unroll
-  for (int i = 0; i < V; ++i) {
-    const int j = mem_idx<V, RB>(i);
-    if (MASKED && pv + j == phead)
-      d = dy[j];
-    else
-      d = fmaf(gs[i], d, dy[j]);
-    float hn = (i == V - 1) ? hnx : h[mem_idx<V, RB>(i + 1)];
-    if (MASKED && pv + j == ptail) hn = 0.0f;
-    dxo[j] = d;
-    dgo[j] = hn * d;
-  }
-  carry = fmaf(ta, carry, tx);
-  carry_g = readlane(g[jl], kWave - 1);
+  float gprev;
+  const SubScan s = bwd_local<IO, RB, MASKED>(g, dy, pv, phead, carry_g, gprev);
+  bwd_apply<IO, RB, MASKED>(g, dy, h, pv, phead, ptail, gprev, hnext_in, s,
+                            carry, dxo, dgo);
+  carry = fmaf(s.ta, carry, s.tx);
+  carry_g = readlane(g[mem_idx<V, RB>(V - 1)], kWave - 1);
 }
 
 template <class IO, bool RB, bool ALN, bool MASKED, int NS>
@@ -483,6 +633,77 @@ __device__ inline void bwd_block(const BwdPtrs& t, const Walk<IO, RB>& w,
   }
 }
 
+// State just past sub-tiles [kk, kk + n) in B order, 0 past the segment.
+template <class IO, bool RB>
+__device__ inline float bwd_halo(const BwdPtrs& t, const Walk<IO, RB>& w,
+                                 int64_t kk, int n) {
+  constexpr int V = IO::V;
+  if (kk + n >= w.nsub) return 0.0f;
+  const int64_t vlast = w.vec(kk + n - 1, kWave - 1);
+  const int64_t pn = RB ? vlast * V - 1 : vlast * V + V;
+  return (pn >= w.P0 && pn < w.P1) ? IO::load1(t.h + pn * IO::ES) : 0.0f;
+}
+
+// Interior sub-tiles of the backward, software-pipelined like fwd_fast.
+template <class IO, bool RB, int U>
+__device__ inline void bwd_fast(const BwdPtrs& t, const Walk<IO, RB>& w,
+                                int64_t k, int64_t kend, int lane,
+                                float& carry, float& carry_g) {
+  constexpr int V = IO::V;
+  constexpr int STEP = RB ? -kWave * 16 : kWave * 16;
+  const uint32_t lo = lane_off<RB>(lane);
+  uint4 ya[U], ga[U], ha[U], yb[U], gb[U], hb[U];
+  float halo_a, halo_b;
+  auto load = [&](uint4(&y)[U], uint4(&g)[U], uint4(&h)[U], float& halo,
+                  int64_t kk) {
+    const int64_t b = sub_lo(w, kk) * 16;
+    const char* yp = t.dy + b + lo;
+    const char* gp = t.g + b + lo;
+    const char* hp = t.h + b + lo;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      y[u] = ld16(yp + u * STEP);
+      g[u] = ld16(gp + u * STEP);
+      h[u] = ld16(hp + u * STEP);
+    }
+    halo = bwd_halo(t, w, kk, U);
+  };
+  auto run = [&](const uint4(&y)[U], const uint4(&g)[U], const uint4(&h)[U],
+                 float halo, int64_t kk) {
+    const int64_t b = sub_lo(w, kk) * 16;
+    char* xp = t.dx + b + lo;
+    char* dp = t.dg + b + lo;
+    float hf[U][V];
+#pragma unroll
+    for (int u = 0; u < U; ++u) IO::unpack(h[u], hf[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float yf[V], gf[V], dx[V], dg[V];
+      IO::unpack(y[u], yf);
+      IO::unpack(g[u], gf);
+      const float hin =
+          (u + 1 < U) ? readlane(hf[u + 1][mem_idx<V, RB>(0)], 0) : halo;
+      bwd_subtile<IO, RB, false>(gf, yf, hf[u], 0, 0, 0, carry, carry_g, hin,
+                                 dx, dg);
+      st16(xp + u * STEP, IO::pack(dx));
+      st16(dp + u * STEP, IO::pack(dg));
+    }
+  };
+  load(ya, ga, ha, halo_a, k);
+  while (true) {
+    const bool more = k + U < kend;
+    if (more) load(yb, gb, hb, halo_b, k + U);
+    run(ya, ga, ha, halo_a, k);
+    k += U;
+    if (!more) break;
+    const bool more2 = k + U < kend;
+    if (more2) load(ya, ga, ha, halo_a, k + U);
+    run(yb, gb, hb, halo_b, k);
+    k += U;
+    if (!more2) break;
+  }
+}
+
 template <class IO, bool RB, bool ALN>
 __device__ void bwd_item(const BwdPtrs& t, int64_t P0, int64_t P1, int lane) {
   constexpr int U = ASC_BWD_UNROLL;
@@ -490,8 +711,16 @@ __device__ void bwd_item(const BwdPtrs& t, int64_t P0, int64_t P1, int lane) {
   float carry = 0.0f, carry_g = 1.0f;
   bwd_block<IO, RB, ALN, true, 1>(t, w, 0, lane, carry, carry_g);
   int64_t k = 1;
-  for (; k + U <= w.kfast; k += U)
-    bwd_block<IO, RB, ALN, false, U>(t, w, k, lane, carry, carry_g);
+  if (ALN) {
+    const int64_t nfull = (w.kfast - 1) / U * U;
+    if (nfull > 0) {
+      bwd_fast<IO, RB, U>(t, w, 1, 1 + nfull, lane, carry, carry_g);
+      k = 1 + nfull;
+    }
+  } else {
+    for (; k + U <= w.kfast; k += U)
+      bwd_block<IO, RB, ALN, false, U>(t, w, k, lane, carry, carry_g);
+  }
   for (; k < w.kfast; ++k)
     bwd_block<IO, RB, ALN, false, 1>(t, w, k, lane, carry, carry_g);
   for (; k < w.nsub; ++k)
@@ -499,9 +728,208 @@ __device__ void bwd_item(const BwdPtrs& t, int64_t P0, int64_t P1, int lane) {
 }
 
 // ---------------------------------------------------------------------------
+// Workgroup-cooperative walk for long segments.  NW waves of one workgroup
+// sweep one item together: in iteration `it`, wave `wv` owns sub-tiles
+// it*NW*kUW + wv*kUW + u (u < kUW), so an iteration streams NW*kUW KiB of
+// every tensor contiguously and far fewer rows are in flight at once than
+// with one wave per item (HBM rewards the fewer, wider streams).  After
+// its wave scans, each wave publishes its aggregate map in LDS; after one
+// barrier every wave folds the aggregates of the waves before it into the
+// iteration carry.  All waves fold the same values in the same order, so
+// they agree bit for bit on the next carry.  The aggregate array is
+// double-buffered by iteration parity: one barrier per iteration suffices.
+// The next iteration's loads are issued before the current one is scanned.
+// ---------------------------------------------------------------------------
+template <class IO, bool REV>
+__device__ inline bool interior(const Walk<IO, REV>& w, int64_t kk) {
+  return kk >= 1 && kk < w.kfast;
+}
+
+template <class IO, bool REV, bool ALN>
+__device__ inline void load_sub(const char* origin, const Walk<IO, REV>& w,
+                                int64_t kk, int lane, float ident, float* f) {
+  const int64_t vi = w.vec(kk, lane);
+  if (interior(w, kk))
+    load_vec<IO, ALN, false>(origin, vi, true, w.P0, w.P1, ident, f);
+  else
+    load_vec<IO, ALN, true>(origin, vi, w.lane_valid(kk, lane), w.P0, w.P1,
+                            ident, f);
+}
+
+template <class IO, bool REV, bool ALN>
+__device__ inline void store_sub(char* origin, const Walk<IO, REV>& w,
+                                 int64_t kk, int lane, const float* f) {
+  const int64_t vi = w.vec(kk, lane);
+  if (interior(w, kk))
+    store_vec<IO, ALN, false>(origin, vi, true, w.P0, w.P1, f);
+  else
+    store_vec<IO, ALN, true>(origin, vi, w.lane_valid(kk, lane), w.P0, w.P1, f);
+}
+
+// Folds the aggregates of waves [0, wv) into `carry` and returns the carry
+// into wave wv; `carry` advances over all NW aggregates.
+template <int NW>
+__device__ inline float fold_aggregates(const float2* slot, int wv,
+                                        float& carry) {
+  float run = carry, mine = carry;
+#pragma unroll
+  for (int j = 0; j < NW; ++j) {
+    if (j == wv) mine = run;
+    const float2 a = slot[j];
+    run = fmaf(a.x, run, a.y);
+  }
+  carry = run;
+  return mine;
+}
+
+template <class IO, bool REV, bool ALN, int NW>
+__device__ void fwd_item_wg(const FwdPtrs& t, int64_t P0, int64_t P1,
+                            int lane, int wv, float2* agg) {
+  constexpr int V = IO::V;
+  constexpr int TS = NW * kUW;
+  const Walk<IO, REV> w(P0, P1);
+  const int64_t niter = (w.nsub + TS - 1) / TS;
+  float gA[kUW][V], xA[kUW][V], gB[kUW][V], xB[kUW][V];
+  float carry = 0.0f;
+  auto load = [&](float(&g)[kUW][V], float(&x)[kUW][V], int64_t it) {
+#pragma unroll
+    for (int u = 0; u < kUW; ++u) {
+      const int64_t kk = it * TS + wv * kUW + u;
+      load_sub<IO, REV, ALN>(t.g, w, kk, lane, 1.0f, g[u]);
+      load_sub<IO, REV, ALN>(t.x, w, kk, lane, 0.0f, x[u]);
+    }
+  };
+  auto step = [&](const float(&g)[kUW][V], const float(&x)[kUW][V],
+                  int64_t it) {
+    SubScan sc[kUW];
+    float wa = 1.0f, wx = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kUW; ++u) {
+      const int64_t kk = it * TS + wv * kUW + u;
+      const int64_t pv = w.vec(kk, lane) * V;
+      if (interior(w, kk))
+        sc[u] = fwd_local<IO, REV, false>(g[u], x[u], pv, 0);
+      else
+        sc[u] = fwd_local<IO, REV, true>(g[u], x[u], pv, w.head());
+      wx = fmaf(sc[u].ta, wx, sc[u].tx);
+      wa = wa * sc[u].ta;
+    }
+    float2* slot = agg + (it & 1) * NW;
+    if (lane == 0) slot[wv] = make_float2(wa, wx);
+    __syncthreads();
+    float c = fold_aggregates<NW>(slot, wv, carry);
+#pragma unroll
+    for (int u = 0; u < kUW; ++u) {
+      const int64_t kk = it * TS + wv * kUW + u;
+      const int64_t pv = w.vec(kk, lane) * V;
+      float hf[V];
+      if (interior(w, kk))
+        fwd_apply<IO, REV, false>(g[u], x[u], pv, 0, sc[u], c, hf);
+      else
+        fwd_apply<IO, REV, true>(g[u], x[u], pv, w.head(), sc[u], c, hf);
+      store_sub<IO, REV, ALN>(t.h, w, kk, lane, hf);
+      c = fmaf(sc[u].ta, c, sc[u].tx);
+    }
+  };
+  load(gA, xA, 0);
+  for (int64_t it = 0;; it += 2) {
+    if (it + 1 < niter) load(gB, xB, it + 1);
+    step(gA, xA, it);
+    if (it + 1 >= niter) break;
+    if (it + 2 < niter) load(gA, xA, it + 2);
+    step(gB, xB, it + 1);
+    if (it + 2 >= niter) break;
+  }
+}
+
+// Gate of the element just before sub-tile kk in B order (1 outside the
+// segment: the pad; the head select makes its value irrelevant there).
+template <class IO, bool RB>
+__device__ inline float bwd_gate_before(const BwdPtrs& t,
+                                        const Walk<IO, RB>& w, int64_t kk) {
+  constexpr int V = IO::V;
+  const int64_t pf = w.vec(kk, 0) * V + mem_idx<V, RB>(0);
+  const int64_t pp = RB ? pf + 1 : pf - 1;
+  return (pp >= w.P0 && pp < w.P1) ? IO::load1(t.g + pp * IO::ES) : 1.0f;
+}
+
+template <class IO, bool RB, bool ALN, int NW>
+__device__ void bwd_item_wg(const BwdPtrs& t, int64_t P0, int64_t P1,
+                            int lane, int wv, float2* agg) {
+  constexpr int V = IO::V;
+  constexpr int TS = NW * kUW;
+  constexpr int jl = mem_idx<V, RB>(V - 1);
+  constexpr int jf = mem_idx<V, RB>(0);
+  const Walk<IO, RB> w(P0, P1);
+  const int64_t niter = (w.nsub + TS - 1) / TS;
+  float yA[kUW][V], gA[kUW][V], hA[kUW][V];
+  float yB[kUW][V], gB[kUW][V], hB[kUW][V];
+  float gpA, hnA, gpB, hnB;
+  float carry = 0.0f;
+  auto load = [&](float(&y)[kUW][V], float(&g)[kUW][V], float(&h)[kUW][V],
+                  float& gp, float& hn, int64_t it) {
+    const int64_t k0 = it * TS + wv * kUW;
+#pragma unroll
+    for (int u = 0; u < kUW; ++u) {
+      load_sub<IO, RB, ALN>(t.dy, w, k0 + u, lane, 0.0f, y[u]);
+      load_sub<IO, RB, ALN>(t.g, w, k0 + u, lane, 1.0f, g[u]);
+      load_sub<IO, RB, ALN>(t.h, w, k0 + u, lane, 0.0f, h[u]);
+    }
+    gp = bwd_gate_before(t, w, k0);
+    hn = bwd_halo(t, w, k0, kUW);
+  };
+  auto step = [&](const float(&y)[kUW][V], const float(&g)[kUW][V],
+                  const float(&h)[kUW][V], float gp, float hn, int64_t it) {
+    const int64_t k0 = it * TS + wv * kUW;
+    SubScan sc[kUW];
+    float gprv[kUW];
+    float wa = 1.0f, wx = 0.0f, cg = gp;
+#pragma unroll
+    for (int u = 0; u < kUW; ++u) {
+      const int64_t pv = w.vec(k0 + u, lane) * V;
+      if (interior(w, k0 + u))
+        sc[u] = bwd_local<IO, RB, false>(g[u], y[u], pv, 0, cg, gprv[u]);
+      else
+        sc[u] = bwd_local<IO, RB, true>(g[u], y[u], pv, w.head(), cg, gprv[u]);
+      cg = readlane(g[u][jl], kWave - 1);
+      wx = fmaf(sc[u].ta, wx, sc[u].tx);
+      wa = wa * sc[u].ta;
+    }
+    float2* slot = agg + (it & 1) * NW;
+    if (lane == 0) slot[wv] = make_float2(wa, wx);
+    __syncthreads();
+    float c = fold_aggregates<NW>(slot, wv, carry);
+#pragma unroll
+    for (int u = 0; u < kUW; ++u) {
+      const int64_t kk = k0 + u;
+      const int64_t pv = w.vec(kk, lane) * V;
+      const float hin = (u + 1 < kUW) ? readlane(h[u + 1][jf], 0) : hn;
+      float dx[V], dg[V];
+      if (interior(w, kk))
+        bwd_apply<IO, RB, false>(g[u], y[u], h[u], pv, 0, 0, gprv[u], hin,
+                                 sc[u], c, dx, dg);
+      else
+        bwd_apply<IO, RB, true>(g[u], y[u], h[u], pv, w.head(), w.tail(),
+                                gprv[u], hin, sc[u], c, dx, dg);
+      store_sub<IO, RB, ALN>(t.dx, w, kk, lane, dx);
+      store_sub<IO, RB, ALN>(t.dg, w, kk, lane, dg);
+      c = fmaf(sc[u].ta, c, sc[u].tx);
+    }
+  };
+  load(yA, gA, hA, gpA, hnA, 0);
+  for (int64_t it = 0;; it += 2) {
+    if (it + 1 < niter) load(yB, gB, hB, gpB, hnB, it + 1);
+    step(yA, gA, hA, gpA, hnA, it);
+    if (it + 1 >= niter) break;
+    if (it + 2 < niter) load(yA, gA, hA, gpA, hnA, it + 2);
+    step(yB, gB, hB, gpB, hnB, it + 1);
+    if (it + 2 >= niter) break;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Kernels.  Work item w (wave-uniform) -> branch, segment s, channel c.
-// Channels vary fastest so that neighbouring waves stream rows of equal
-// length.  DIRS: 1 = all items forward-direction, 2 = all reverse,
+// DIRS: 1 = all items forward-direction, 2 = all reverse,
 // 3 = branch 0 forward / branch 1 reverse (fused bidirectional launch).
 // ---------------------------------------------------------------------------
 struct Geometry {
@@ -513,18 +941,39 @@ struct Geometry {
   int phase;
 };
 
-__device__ inline int64_t cu_at(const Geometry& geo, int64_t i) {
-  return geo.cu64 ? reinterpret_cast<const int64_t*>(geo.cu)[i]
-                  : static_cast<int64_t>(reinterpret_cast<const int32_t*>(geo.cu)[i]);
+// Tells the compiler a value is the same in every lane (it is: all lanes
+// of a wave work on the same item), so that item geometry and base
+// addresses live in scalar registers.
+__device__ inline int64_t uniform(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// Decodes item w; returns false for an empty segment.
+__device__ inline int64_t cu_at(const Geometry& geo, int64_t i) {
+  return uniform(geo.cu64
+                     ? reinterpret_cast<const int64_t*>(geo.cu)[i]
+                     : static_cast<int64_t>(reinterpret_cast<const int32_t*>(geo.cu)[i]));
+}
+
+// Decodes item w; returns false for an empty segment.  SEG_MAJOR: items
+// w, w+1 are neighbouring segments of one row, so waves that run at the
+// same time stream neighbouring memory (the order used for short items);
+// otherwise they are the same segment of neighbouring channels.
+template <bool SEG_MAJOR>
 __device__ inline bool item_range(const Geometry& geo, int64_t w, int& br,
                                   int64_t& P0, int64_t& P1) {
   br = w >= geo.items ? 1 : 0;
   const int64_t r = w - br * geo.items;
-  const int64_t s = r / geo.C;
-  const int64_t c = r - s * geo.C;
+  int64_t s, c;
+  if (SEG_MAJOR) {
+    c = r / geo.S;
+    s = r - c * geo.S;
+  } else {
+    s = r / geo.C;
+    c = r - s * geo.C;
+  }
   int64_t t0 = cu_at(geo, s), t1 = cu_at(geo, s + 1);
   t0 = t0 < 0 ? 0 : (t0 > geo.T ? geo.T : t0);
   t1 = t1 < t0 ? t0 : (t1 > geo.T ? geo.T : t1);
@@ -552,7 +1001,7 @@ __global__ void __launch_bounds__(kWPB* kWave) k_scan_fwd(FwdParams p) {
        w += stride) {
     int br;
     int64_t P0, P1;
-    if (!item_range(p.geo, w, br, P0, P1)) continue;
+    if (!item_range<true>(p.geo, w, br, P0, P1)) continue;
     const FwdPtrs& t = p.br[br];
     if (DIRS == 1 || (DIRS == 3 && br == 0))
       fwd_item<IO, false, ALN, WA>(t, P0, P1, lane);
@@ -578,12 +1027,51 @@ __global__ void __launch_bounds__(kWPB* kWave) k_scan_bwd(BwdParams p) {
        w += stride) {
     int br;
     int64_t P0, P1;
-    if (!item_range(p.geo, w, br, P0, P1)) continue;
+    if (!item_range<true>(p.geo, w, br, P0, P1)) continue;
     const BwdPtrs& t = p.br[br];
     if (DIRS == 1 || (DIRS == 3 && br == 0))
       bwd_item<IO, true, ALN>(t, P0, P1, lane);
     else
       bwd_item<IO, false, ALN>(t, P0, P1, lane);
+  }
+}
+
+// Workgroup-cooperative kernels: one item per workgroup of NW waves.
+template <class IO, int DIRS, bool ALN, int NW>
+__global__ void __launch_bounds__(NW* kWave) k_scan_fwd_wg(FwdParams p) {
+  __shared__ float2 agg[2 * NW];
+  const int lane = threadIdx.x % kWave;
+  const int wv = wave_id();
+  const int64_t W = p.geo.items * p.geo.nbranch;
+  for (int64_t item = blockIdx.x; item < W; item += gridDim.x) {
+    int br;
+    int64_t P0, P1;
+    if (!item_range<false>(p.geo, item, br, P0, P1)) continue;
+    const FwdPtrs& t = p.br[br];
+    if (DIRS == 1 || (DIRS == 3 && br == 0))
+      fwd_item_wg<IO, false, ALN, NW>(t, P0, P1, lane, wv, agg);
+    else
+      fwd_item_wg<IO, true, ALN, NW>(t, P0, P1, lane, wv, agg);
+    __syncthreads();  // agg is reused by the next item
+  }
+}
+
+template <class IO, int DIRS, bool ALN, int NW>
+__global__ void __launch_bounds__(NW* kWave) k_scan_bwd_wg(BwdParams p) {
+  __shared__ float2 agg[2 * NW];
+  const int lane = threadIdx.x % kWave;
+  const int wv = wave_id();
+  const int64_t W = p.geo.items * p.geo.nbranch;
+  for (int64_t item = blockIdx.x; item < W; item += gridDim.x) {
+    int br;
+    int64_t P0, P1;
+    if (!item_range<false>(p.geo, item, br, P0, P1)) continue;
+    const BwdPtrs& t = p.br[br];
+    if (DIRS == 1 || (DIRS == 3 && br == 0))
+      bwd_item_wg<IO, true, ALN, NW>(t, P0, P1, lane, wv, agg);
+    else
+      bwd_item_wg<IO, false, ALN, NW>(t, P0, P1, lane, wv, agg);
+    __syncthreads();
   }
 }
 
@@ -727,15 +1215,66 @@ int check_ptrs(const void* const* ptrs, int n, int es) {
 }
 
 template <class Params>
-int launch(const void* fn, int64_t items, int waves_per_block, Params& p,
+int launch(const void* fn, int64_t blocks, int waves_per_block, Params& p,
            void* stream) {
-  int64_t blocks = (items + waves_per_block - 1) / waves_per_block;
   if (blocks > kMaxGrid) blocks = kMaxGrid;
   void* args[] = {&p};
   const hipError_t e = hipLaunchKernel(fn, dim3(static_cast<unsigned>(blocks)),
                                        dim3(waves_per_block * kWave), args, 0,
                                        static_cast<hipStream_t>(stream));
   return e == hipSuccess ? ASC_OK : static_cast<int>(e);
+}
+
+// Walk selection from the mean segment length (host-side, no sync).  The
+// workgroup-cooperative walk pays one barrier per iteration and an
+// unoverlapped first load per item, so it needs several iterations per item
+// to beat one wave per item; the thresholds below are in iterations of the
+// 16-wave and 8-wave tiles and were set by measurement on MI355X.
+// Returns the waves per workgroup, or 0 for one wave per item.
+#ifndef ASC_FWD_WG16_MIN_ITERS
+#define ASC_FWD_WG16_MIN_ITERS 8
+#endif
+#ifndef ASC_BWD_WG16_MIN_ITERS
+#define ASC_BWD_WG16_MIN_ITERS 4
+#endif
+#ifndef ASC_WG8_MIN_ITERS
+#define ASC_WG8_MIN_ITERS 4
+#endif
+int pick_walk(int64_t S, int64_t T, int v, bool bwd) {
+  const int64_t mean = T / (S > 0 ? S : 1);
+  const int64_t tile1 = static_cast<int64_t>(kUW) * kWave * v;  // per wave
+  const int64_t it16 = bwd ? ASC_BWD_WG16_MIN_ITERS : ASC_FWD_WG16_MIN_ITERS;
+  if (mean >= it16 * 16 * tile1) return 16;
+  if (mean >= static_cast<int64_t>(ASC_WG8_MIN_ITERS) * 8 * tile1) return 8;
+  return 0;
+}
+
+template <class IO, int NW>
+const void* pick_fwd_wg(int dirs, bool aln) {
+#define ASC_F(D, A) reinterpret_cast<const void*>(&k_scan_fwd_wg<IO, D, A, NW>)
+  if (dirs == 1) return aln ? ASC_F(1, true) : ASC_F(1, false);
+  if (dirs == 2) return aln ? ASC_F(2, true) : ASC_F(2, false);
+  return aln ? ASC_F(3, true) : ASC_F(3, false);
+#undef ASC_F
+}
+
+template <class IO, int NW>
+const void* pick_bwd_wg(int dirs, bool aln) {
+#define ASC_B(D, A) reinterpret_cast<const void*>(&k_scan_bwd_wg<IO, D, A, NW>)
+  if (dirs == 1) return aln ? ASC_B(1, true) : ASC_B(1, false);
+  if (dirs == 2) return aln ? ASC_B(2, true) : ASC_B(2, false);
+  return aln ? ASC_B(3, true) : ASC_B(3, false);
+#undef ASC_B
+}
+
+template <class IO>
+const void* pick_fwd_wg(int nw, int dirs, bool aln) {
+  return nw == 16 ? pick_fwd_wg<IO, 16>(dirs, aln) : pick_fwd_wg<IO, 8>(dirs, aln);
+}
+
+template <class IO>
+const void* pick_bwd_wg(int nw, int dirs, bool aln) {
+  return nw == 16 ? pick_bwd_wg<IO, 16>(dirs, aln) : pick_bwd_wg<IO, 8>(dirs, aln);
 }
 
 template <class IO>
@@ -794,13 +1333,24 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
     p.br[b].a = (b == 0 && a) ? static_cast<char*>(a) - shift : nullptr;
   }
   const bool wa = a != nullptr;
+  const int64_t items = p.geo.items * nbranch;
+  const int nw = wa ? 0 : pick_walk(S, T, v, false);
+  if (nw) {
+    const void* fn = nullptr;
+    switch (dtype) {
+      case ASC_F32: fn = pick_fwd_wg<IoF32>(nw, dirs, aln); break;
+      case ASC_F16: fn = pick_fwd_wg<IoF16>(nw, dirs, aln); break;
+      default: fn = pick_fwd_wg<IoBF16>(nw, dirs, aln); break;
+    }
+    return launch(fn, items, nw, p, stream);
+  }
   const void* fn = nullptr;
   switch (dtype) {
     case ASC_F32: fn = pick_fwd<IoF32>(dirs, aln, wa); break;
     case ASC_F16: fn = pick_fwd<IoF16>(dirs, aln, wa); break;
     default: fn = pick_fwd<IoBF16>(dirs, aln, wa); break;
   }
-  return launch(fn, p.geo.items * nbranch, kWPB, p, stream);
+  return launch(fn, (items + kWPB - 1) / kWPB, kWPB, p, stream);
 }
 
 int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
@@ -837,13 +1387,24 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
     p.br[b].dx = static_cast<char*>(dx[b]) - shift;
     p.br[b].dg = static_cast<char*>(dg[b]) - shift;
   }
+  const int64_t items = p.geo.items * nbranch;
+  const int nw = pick_walk(S, T, v, true);
+  if (nw) {
+    const void* fn = nullptr;
+    switch (dtype) {
+      case ASC_F32: fn = pick_bwd_wg<IoF32>(nw, dirs, aln); break;
+      case ASC_F16: fn = pick_bwd_wg<IoF16>(nw, dirs, aln); break;
+      default: fn = pick_bwd_wg<IoBF16>(nw, dirs, aln); break;
+    }
+    return launch(fn, items, nw, p, stream);
+  }
   const void* fn = nullptr;
   switch (dtype) {
     case ASC_F32: fn = pick_bwd<IoF32>(dirs, aln); break;
     case ASC_F16: fn = pick_bwd<IoF16>(dirs, aln); break;
     default: fn = pick_bwd<IoBF16>(dirs, aln); break;
   }
-  return launch(fn, p.geo.items * nbranch, kWPB, p, stream);
+  return launch(fn, (items + kWPB - 1) / kWPB, kWPB, p, stream);
 }
 
 }  // namespace
@@ -949,7 +1510,7 @@ int asc_shift_pad(const void* data, void* out, const void* cu_seqlens,
     case ASC_F16: fn = reinterpret_cast<const void*>(&k_shift_pad<IoF16>); break;
     default: fn = reinterpret_cast<const void*>(&k_shift_pad<IoBF16>); break;
   }
-  return launch(fn, p.C * p.chunks, 4, p, stream);
+  return launch(fn, (p.C * p.chunks + 3) / 4, 4, p, stream);
 }
 
 }  // extern "C"

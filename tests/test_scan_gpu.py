@@ -41,6 +41,11 @@ LENS = [
   [1000, 3, 4097],
   [17, 1, 2, 3, 1024, 1025, 250],
   [2 * 4096 + 3, 7],
+  # long segments: walked by the workgroup-cooperative kernels (fp32 from a
+  # mean of 16384 elements, fp16/bf16 from 32768), with short segments mixed in
+  [20000],
+  [16384 * 2 + 5],
+  [70000, 1, 2, 5000, 100000],
 ]
 
 
@@ -130,10 +135,15 @@ def test_forward_parity(dtype, reverse, lens):
   a = torch.empty_like(gd)
   cu = torch.tensor(cu_of(lens), device=DEV, dtype=torch.int32)
   from associative_scan_triton import _ops
-  _ops.scan_fwd(gd, xd, h, cu, reverse=reverse, gate_prod_out=a)
   ref, a_ref = oracle.scan_fwd(npf(g), npf(x), cu_of(lens), reverse,
                                gate_prod=True)
+  # without the gate product (long segments take the workgroup walk) ...
+  _ops.scan_fwd(gd, xd, h, cu, reverse=reverse)
   check_close(h, ref, dtype, "h")
+  # ... and with it (always the one-wave-per-segment walk)
+  h2 = torch.empty_like(xd)
+  _ops.scan_fwd(gd, xd, h2, cu, reverse=reverse, gate_prod_out=a)
+  check_close(h2, ref, dtype, "h (with gate product)")
   check_close(a, a_ref, dtype, "gate product")
   assert torch.equal(gd, g.to(DEV)) and torch.equal(xd, x.to(DEV))
 
@@ -283,8 +293,9 @@ def test_nonfinite_values_stay_in_their_segment():
 @pytest.mark.parametrize("offsets", [(1, 1, 1), (2, 2, 2), (3, 1, 2), (0, 1, 0)],
                          ids=["phase1", "phase2", "mixed", "mixed2"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
-def test_misaligned_views(offsets, dtype):
-  lens = [700, 1, 33, 1500]
+@pytest.mark.parametrize("lens", [[700, 1, 33, 1500], [40000, 3, 90001]],
+                         ids=["short", "long"])
+def test_misaligned_views(offsets, dtype, lens):
   C = 3
   T = sum(lens)
   g, x, dy = make(lens, C, dtype, n=3)

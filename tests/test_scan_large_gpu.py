@@ -33,9 +33,8 @@ def _check_fwd_bwd(g, x, dy, h, dx, dg, cu, dtype, rows, reverse=False):
   check_close(h[rows], h_ref, dtype, "h (sampled rows)")
   dx_ref, dg_ref = oracle.scan_bwd(dys, gs, npf(h[rows]), cu_np,
                                    causal=not reverse)
-  scale = max(1.0, float(np.abs(dx_ref).max()) * 1e-2)
-  check_close(dx[rows], dx_ref, dtype, "dx (sampled rows)", scale)
-  check_close(dg[rows], dg_ref, dtype, "dg (sampled rows)", scale)
+  check_close(dx[rows], dx_ref, dtype, "dx (sampled rows)")
+  check_close(dg[rows], dg_ref, dtype, "dg (sampled rows)")
   # whole tensor: exact heads, all finite
   heads = cu[1:].long() - 1 if reverse else cu[:-1].long()
   assert torch.equal(h[:, heads], x[:, heads])
@@ -130,3 +129,34 @@ def test_cfg1_small_causal():
   check_close(y, h_ref, torch.float32, "h")
   check_close(xd.grad, dx_ref, torch.float32, "dx")
   check_close(gd.grad, dg_ref, torch.float32, "dg")
+
+
+def test_long_memory_error_vs_sequential_fp32():
+  """Gates in (0.99, 1) (cfg5's long-memory regime): the kernels' fp32 error
+  against the fp64 oracle is no worse than that of a sequential fp32 scan
+  (one rounding per operation) on the same inputs -- the bar a Triton or any
+  other fp32-accumulating scan is held to.  Compared by max absolute error
+  and RMSE over 32 full rows of 8 x 65536."""
+  C, B, T = 32, 8, 65536
+  gen = _gen(11)
+  g = torch.rand(C, B * T, device=DEV, generator=gen).mul_(0.01).add_(0.99)
+  x = torch.randn(C, B * T, device=DEV, generator=gen)
+  cu = torch.arange(B + 1, device=DEV, dtype=torch.int32) * T
+  h = torch.empty_like(x)
+  _ops.scan_fwd(g, x, h, cu, reverse=False)
+  gn, xn = g.cpu().numpy(), x.cpu().numpy()
+  ref = oracle.scan_fwd(gn.astype(np.float64), xn.astype(np.float64),
+                        cu.cpu().numpy().astype(np.int64))
+  seq = np.empty_like(xn)
+  for s in range(B):
+    hh = xn[:, s * T].copy()
+    seq[:, s * T] = hh
+    for t in range(s * T + 1, (s + 1) * T):
+      hh = gn[:, t] * hh + xn[:, t]
+      seq[:, t] = hh
+  e_gpu = np.abs(npf(h) - ref)
+  e_seq = np.abs(seq.astype(np.float64) - ref)
+  assert e_gpu.max() <= e_seq.max(), (e_gpu.max(), e_seq.max())
+  assert np.sqrt(np.mean(e_gpu ** 2)) <= np.sqrt(np.mean(e_seq ** 2))
+  # normwise: within rtol 1e-5 of the value scale of each row
+  assert (e_gpu.max(1) / np.abs(ref).max(1)).max() < 1e-5
