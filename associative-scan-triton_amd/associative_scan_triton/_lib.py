@@ -17,7 +17,7 @@ from associative_scan_triton._build import LIB_PATH
 
 ASC_F32, ASC_F16, ASC_BF16 = 0, 1, 2
 ASC_CU_I32, ASC_CU_I64 = 0, 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _DTYPES = {
   torch.float32: ASC_F32,
@@ -31,14 +31,23 @@ _L = ctypes.c_int64
 _D = ctypes.c_double
 
 # name -> argtypes, mirroring include/assocscan.h
+_U = ctypes.c_uint
+
 SIGNATURES = {
   "asc_abi_version": [],
+  "asc_scan_workspace_bytes": [_L, _L, _L, _I, _I],
+  "asc_set_lookback_spin_limit": [_U],
   "asc_strerror": [_I],
-  "asc_scan_fwd": [_P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P],
-  "asc_scan_bwd": [_P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P],
-  "asc_scan_bidi_fwd": [_P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _P],
-  "asc_scan_bidi_bwd": [_P] * 11 + [_I, _L, _L, _L, _I, _P],
+  "asc_scan_fwd": [_P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P, _L, _P],
+  "asc_scan_bwd": [_P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P, _L, _P],
+  "asc_scan_bidi_fwd": [_P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _P, _L, _P],
+  "asc_scan_bidi_bwd": [_P] * 11 + [_I, _L, _L, _L, _I, _P, _L, _P],
   "asc_shift_pad": [_P, _P, _P, _I, _L, _L, _L, _I, _D, _I, _I, _P],
+}
+RESTYPES = {
+  "asc_strerror": ctypes.c_char_p,
+  "asc_scan_workspace_bytes": ctypes.c_int64,
+  "asc_set_lookback_spin_limit": ctypes.c_uint,
 }
 
 _lib = None
@@ -66,7 +75,7 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
     for name, argtypes in SIGNATURES.items():
       fn = getattr(lib, name)
       fn.argtypes = argtypes
-      fn.restype = ctypes.c_char_p if name == "asc_strerror" else ctypes.c_int
+      fn.restype = RESTYPES.get(name, ctypes.c_int)
     if lib.asc_abi_version() != ABI_VERSION:
       raise RuntimeError(
         f"libassocscan ABI {lib.asc_abi_version()} != expected {ABI_VERSION}")

@@ -12,6 +12,24 @@ import torch
 
 from associative_scan_triton import _lib
 
+# Problems with few (segment, channel) items run the library's look-back walk,
+# which needs a workspace; the library says how large (0 = none needed).
+# False forces the workspace-free walks (the two agree to fp32 rounding).
+USE_WORKSPACE = True
+
+
+def _workspace(lib, dev: torch.device, S: int, C: int, T: int,
+               dtype_code: int, nbranch: int):
+  """A workspace from torch's caching allocator when the geometry wants one
+  (the library clears it on the launch stream), else (None, 0)."""
+  if not USE_WORKSPACE:
+    return None, 0
+  nbytes = lib.asc_scan_workspace_bytes(S, C, T, dtype_code, nbranch)
+  if nbytes <= 0:
+    return None, 0
+  ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+  return ws, nbytes
+
 
 def _geometry(t: torch.Tensor, cu: torch.Tensor, num_channels: int | None
               ) -> tuple[int, int, int]:
@@ -83,10 +101,11 @@ def scan_fwd(gates: torch.Tensor, tokens: torch.Tensor, h_out: torch.Tensor,
   cu = cu.contiguous()
   S, C, T = _geometry(tokens, cu, num_channels)
   with _OnDevice(dev):
+    ws, nb = (None, 0) if gate_prod_out is not None else _workspace(lib, dev, S, C, T, dt, 1)
     _lib.check(lib.asc_scan_fwd(
       gates.data_ptr(), tokens.data_ptr(), h_out.data_ptr(),
       _lib.ptr(gate_prod_out), cu.data_ptr(), cuc, S, C, T, dt,
-      1 if reverse else 0, _lib.stream_of(dev)))
+      1 if reverse else 0, _lib.ptr(ws), nb, _lib.stream_of(dev)))
 
 
 def scan_bwd(grad: torch.Tensor, gates: torch.Tensor, states: torch.Tensor,
@@ -101,10 +120,11 @@ def scan_bwd(grad: torch.Tensor, gates: torch.Tensor, states: torch.Tensor,
   cu = cu.contiguous()
   S, C, T = _geometry(grad, cu, num_channels)
   with _OnDevice(dev):
+    ws, nb = _workspace(lib, dev, S, C, T, dt, 1)
     _lib.check(lib.asc_scan_bwd(
       grad.data_ptr(), gates.data_ptr(), states.data_ptr(),
       d_tokens.data_ptr(), d_gates.data_ptr(), cu.data_ptr(), cuc, S, C, T,
-      dt, 1 if causal else 0, _lib.stream_of(dev)))
+      dt, 1 if causal else 0, _lib.ptr(ws), nb, _lib.stream_of(dev)))
 
 
 def scan_bidi_fwd(gf: torch.Tensor, xf: torch.Tensor, gb: torch.Tensor,
@@ -119,10 +139,11 @@ def scan_bidi_fwd(gf: torch.Tensor, xf: torch.Tensor, gb: torch.Tensor,
   cu = cu.contiguous()
   S, C, T = _geometry(xf, cu, num_channels)
   with _OnDevice(dev):
+    ws, nb = _workspace(lib, dev, S, C, T, dt, 2)
     _lib.check(lib.asc_scan_bidi_fwd(
       gf.data_ptr(), xf.data_ptr(), gb.data_ptr(), xb.data_ptr(),
       hf.data_ptr(), hb.data_ptr(), cu.data_ptr(), cuc, S, C, T, dt,
-      _lib.stream_of(dev)))
+      _lib.ptr(ws), nb, _lib.stream_of(dev)))
 
 
 def scan_bidi_bwd(dyf: torch.Tensor, dyb: torch.Tensor, gf: torch.Tensor,
@@ -139,11 +160,12 @@ def scan_bidi_bwd(dyf: torch.Tensor, dyb: torch.Tensor, gf: torch.Tensor,
   cu = cu.contiguous()
   S, C, T = _geometry(dyf, cu, num_channels)
   with _OnDevice(dev):
+    ws, nb = _workspace(lib, dev, S, C, T, dt, 2)
     _lib.check(lib.asc_scan_bidi_bwd(
       dyf.data_ptr(), dyb.data_ptr(), gf.data_ptr(), gb.data_ptr(),
       hf.data_ptr(), hb.data_ptr(), dxf.data_ptr(), dgf.data_ptr(),
       dxb.data_ptr(), dgb.data_ptr(), cu.data_ptr(), cuc, S, C, T, dt,
-      _lib.stream_of(dev)))
+      _lib.ptr(ws), nb, _lib.stream_of(dev)))
 
 
 def shift_pad(data: torch.Tensor, out: torch.Tensor, cu: torch.Tensor,

@@ -17,6 +17,17 @@
  * ASC_E_* code for an invalid argument (nothing is launched), or a positive
  * hipError_t from the launch.  asc_strerror() turns any of them into text.
  *
+ * Workspace: the scan entry points take an optional caller-owned device
+ * buffer (32-byte aligned, asc_scan_workspace_bytes() bytes).  Problems
+ * with few (segment, channel) items -- one long sequence, a handful of
+ * channels -- need it: with it they run a single-pass decoupled look-back
+ * walk over tiles of 1024 elements that keeps every CU busy (the buffer
+ * holds one 16-byte carry slot per tile and is cleared by the call itself,
+ * on `stream`).  Every other problem, and any call given NULL or a buffer
+ * too small, runs the workspace-free walks (one wave or one workgroup per
+ * item).  Results agree to fp32 rounding.  Two calls that run at the same
+ * time must not share a workspace.
+ *
  * The reference is the Triton package associative-scan-triton 1.0.0; the
  * citations below name the reference function each entry point replaces.
  */
@@ -53,8 +64,28 @@ enum {
 };
 
 /* ABI version of this header; bumped on any signature change. */
-#define ASC_ABI_VERSION 1
+#define ASC_ABI_VERSION 2
 int asc_abi_version(void);
+
+/*
+ * Workspace bytes a scan entry point wants for this geometry, for
+ * nbranch = 1 (asc_scan_fwd / asc_scan_bwd) or 2 (the bidirectional calls):
+ * 0 when it runs a workspace-free walk anyway, a negative ASC_E_* code for
+ * invalid arguments.  No reference counterpart: the reference's Triton
+ * kernels carry their chunk carry in registers of one program per
+ * (sequence, channel) and need no workspace.
+ */
+int64_t asc_scan_workspace_bytes(int64_t num_seq, int64_t num_channels,
+                                 int64_t seq_stride, int dtype, int nbranch);
+
+/*
+ * Test hook, no reference counterpart: sets how many times a look-back wave
+ * polls a preceding tile's slot before it computes that tile's carry map
+ * from the tile's inputs itself (0 = always compute; the default keeps the
+ * fallback for pathological scheduling only).  Returns the previous value.
+ * Affects launches issued after the call.
+ */
+unsigned asc_set_lookback_spin_limit(unsigned polls);
 
 /* Human-readable text for a status code returned by any entry point. */
 const char* asc_strerror(int status);
@@ -66,7 +97,8 @@ const char* asc_strerror(int status);
  * gate_prod_out (nullable): also writes the running gate product
  *   A[t] = prod g over [start..t] (reverse: over [t..end-1]).
  * In-place use is allowed: h_out may equal tokens and gate_prod_out may
- * equal gates (each element is read before it is overwritten).
+ * equal gates (each element is read before it is overwritten).  With
+ * gate_prod_out the workspace-free walk is used.
  *
  * Replaces: _dispatcher.py:12-70 forward_scan_full, which launches
  *   _kernels.py:19-81  forward_scan_chunked (one chunk) or
@@ -77,7 +109,8 @@ const char* asc_strerror(int status);
 int asc_scan_fwd(const void* gates, const void* tokens, void* h_out,
                  void* gate_prod_out, const void* cu_seqlens, int cu_dtype,
                  int64_t num_seq, int64_t num_channels, int64_t seq_stride,
-                 int dtype, int reverse, void* stream);
+                 int dtype, int reverse, void* workspace,
+                 int64_t workspace_bytes, void* stream);
 
 /*
  * Fused backward of a forward scan (reads dy, g, h once; writes dx, dg).
@@ -95,7 +128,8 @@ int asc_scan_fwd(const void* gates, const void* tokens, void* h_out,
 int asc_scan_bwd(const void* grad, const void* gates, const void* states,
                  void* d_tokens, void* d_gates, const void* cu_seqlens,
                  int cu_dtype, int64_t num_seq, int64_t num_channels,
-                 int64_t seq_stride, int dtype, int causal, void* stream);
+                 int64_t seq_stride, int dtype, int causal, void* workspace,
+                 int64_t workspace_bytes, void* stream);
 
 /*
  * Both branches of the bidirectional scan in ONE launch: a causal scan of
@@ -109,7 +143,8 @@ int asc_scan_bidi_fwd(const void* gates_fwd, const void* tokens_fwd,
                       const void* gates_bwd, const void* tokens_bwd,
                       void* h_fwd, void* h_bwd, const void* cu_seqlens,
                       int cu_dtype, int64_t num_seq, int64_t num_channels,
-                      int64_t seq_stride, int dtype, void* stream);
+                      int64_t seq_stride, int dtype, void* workspace,
+                      int64_t workspace_bytes, void* stream);
 
 /*
  * Backward of both bidirectional branches in ONE launch: causal backward of
@@ -125,7 +160,7 @@ int asc_scan_bidi_bwd(const void* grad_fwd, const void* grad_bwd,
                       void* d_tokens_bwd, void* d_gates_bwd,
                       const void* cu_seqlens, int cu_dtype, int64_t num_seq,
                       int64_t num_channels, int64_t seq_stride, int dtype,
-                      void* stream);
+                      void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Segment-aware shift by one position with padding, on a contiguous

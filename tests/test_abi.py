@@ -39,7 +39,7 @@ def test_exports_every_declared_symbol():
 
 def test_abi_version_and_strerror():
   lib = _lib.load()
-  assert lib.asc_abi_version() == 1
+  assert lib.asc_abi_version() == 2
   assert lib.asc_strerror(0) == b"success"
   for code in (-1, -2, -3, -4, -5):
     assert lib.asc_strerror(code) and lib.asc_strerror(code) != b"unknown error"
@@ -48,7 +48,7 @@ def test_abi_version_and_strerror():
 
 def _fwd(lib, **kw):
   a = dict(gates=8, tokens=8, h_out=8, gate_prod_out=None, cu=8, cu_dtype=0,
-           S=1, C=1, T=4, dtype=0, reverse=0, stream=None)
+           S=1, C=1, T=4, dtype=0, reverse=0, ws=None, ws_bytes=0, stream=None)
   a.update(kw)
   return lib.asc_scan_fwd(*a.values())
 
@@ -66,8 +66,32 @@ def test_host_validation_codes():
   # empty problems are a successful no-op (nothing is launched)
   assert _fwd(lib, S=0) == 0
   assert _fwd(lib, C=0) == 0
-  assert lib.asc_scan_bwd(8, 8, 8, 8, None, 8, 0, 1, 1, 4, 0, 1, None) == -1
+  assert lib.asc_scan_bwd(8, 8, 8, 8, None, 8, 0, 1, 1, 4, 0, 1, None, 0,
+                          None) == -1
   assert lib.asc_shift_pad(8, 8, 8, 0, 1, 1, 4, 5, 0.0, 1, 1, None) == -2
+
+
+def test_workspace_bytes():
+  lib = _lib.load()
+  # few (segment, channel) items: one 16-byte slot per tile of 1024 elements
+  # (counted for the worst-case phase), per branch
+  n = 4 * 1_000_000
+  b1 = lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 0, 1)
+  b2 = lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 0, 2)
+  assert b1 == 16 * -(-(n + 3) // 1024) and b2 == 2 * b1
+  assert lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 2, 1) == 16 * -(-(n + 7) // 1024)
+  # many items: the workspace-free walks, no workspace
+  assert lib.asc_scan_workspace_bytes(8, 1536, 524288, 0, 1) == 0
+  assert lib.asc_scan_workspace_bytes(1, 64, 4096, 0, 1) == 0
+  assert lib.asc_scan_workspace_bytes(1, 32, 4096, 0, 2) == 0
+  assert lib.asc_scan_workspace_bytes(1, 63, 4096, 0, 1) > 0
+  # empty problems need nothing; invalid arguments are errors
+  assert lib.asc_scan_workspace_bytes(0, 4, 128, 0, 1) == 0
+  assert lib.asc_scan_workspace_bytes(1, 4, 128, 9, 1) < 0
+  assert lib.asc_scan_workspace_bytes(1, 4, 128, 0, 3) < 0
+  assert lib.asc_scan_workspace_bytes(-1, 4, 128, 0, 1) < 0
+  prev = lib.asc_set_lookback_spin_limit(7)
+  assert lib.asc_set_lookback_spin_limit(prev) == 7
 
 
 def test_error_is_raised_with_message():

@@ -124,10 +124,21 @@ def test_golden_causal_grad(case, compiled):
 # random parity against the fp64 oracle
 # ---------------------------------------------------------------------------
 
+@pytest.fixture(params=["lookback", "direct"])
+def walk(request):
+  """Runs a test with the workspace (decoupled look-back walk) and without
+  it (one wave or one workgroup per segment)."""
+  from associative_scan_triton import _ops
+  prev = _ops.USE_WORKSPACE
+  _ops.USE_WORKSPACE = request.param == "lookback"
+  yield request.param
+  _ops.USE_WORKSPACE = prev
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("reverse", [False, True], ids=["causal", "reverse"])
 @pytest.mark.parametrize("lens", LENS, ids=lambda l: "x".join(map(str, l))[:40])
-def test_forward_parity(dtype, reverse, lens):
+def test_forward_parity(dtype, reverse, lens, walk):
   C = 3
   g, x = make(lens, C, dtype)
   gd, xd = g.to(DEV), x.to(DEV)
@@ -151,7 +162,7 @@ def test_forward_parity(dtype, reverse, lens):
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "anticausal"])
 @pytest.mark.parametrize("lens", LENS, ids=lambda l: "x".join(map(str, l))[:40])
-def test_backward_parity(dtype, causal, lens):
+def test_backward_parity(dtype, causal, lens, walk):
   C = 3
   g, h, dy = make(lens, C, dtype, n=3)
   dx = torch.empty(C, sum(lens), dtype=dtype, device=DEV)
@@ -186,7 +197,7 @@ def test_scan_causal_autograd_parity(dtype, lens):
 @pytest.mark.parametrize("compiled", [False, True], ids=["eager", "compiled"])
 @pytest.mark.parametrize("lens", [[5], [64, 1, 300], [2048, 33]],
                          ids=lambda l: "x".join(map(str, l)))
-def test_bidirectional_parity(dtype, compiled, lens):
+def test_bidirectional_parity(dtype, compiled, lens, walk):
   C = 3
   gf, xf, dyf = make(lens, C, dtype, seed=1, glo=0.9, n=3)
   gb, xb, dyb = make(lens, C, dtype, seed=2, glo=0.9, n=3)
@@ -230,7 +241,7 @@ def test_bidirectional_compiled_matches_eager():
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
-def test_segment_boundaries_bit_exact(dtype):
+def test_segment_boundaries_bit_exact(dtype, walk):
   lens = [1, 2, 3, 257, 64, 1, 513, 9]
   C = 5
   g, x, dy = make(lens, C, dtype, n=3, glo=-2.0, ghi=2.0)
@@ -261,7 +272,7 @@ def test_segment_boundaries_bit_exact(dtype):
     assert torch.equal(dg[:, last].cpu().view(iv), exp.cpu().view(iv))
 
 
-def test_nonfinite_values_stay_in_their_segment():
+def test_nonfinite_values_stay_in_their_segment(walk):
   lens = [300, 5, 700, 1]
   C = 2
   g, x, dy = make(lens, C, n=3)
@@ -295,7 +306,7 @@ def test_nonfinite_values_stay_in_their_segment():
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("lens", [[700, 1, 33, 1500], [40000, 3, 90001]],
                          ids=["short", "long"])
-def test_misaligned_views(offsets, dtype, lens):
+def test_misaligned_views(offsets, dtype, lens, walk):
   C = 3
   T = sum(lens)
   g, x, dy = make(lens, C, dtype, n=3)
@@ -563,3 +574,34 @@ def test_stream_semantics():
     _ops.scan_fwd(gd, xd, h, torch.tensor(cu_of(lens), device=DEV), False)
   s.synchronize()
   check_close(h, oracle_fwd(g, x, lens), torch.float32, "h on side stream")
+
+
+@pytest.mark.parametrize("lens", [[5000], [20000, 3, 1, 7000], [1, 2, 3, 4, 5, 900]],
+                         ids=["one", "mixed", "short"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_lookback_fallback_path(lens, dtype):
+  """With a spin limit of 0 every look-back that finds a predecessor not yet
+  published computes that tile's map from its inputs (the bounded-wait
+  path that guarantees progress).  Results must not change."""
+  from associative_scan_triton import _lib, _ops
+  lib = _lib.load()
+  prev_ws = _ops.USE_WORKSPACE
+  _ops.USE_WORKSPACE = True
+  prev = lib.asc_set_lookback_spin_limit(0)
+  try:
+    C = 5
+    g, x, dy = make(lens, C, dtype, n=3, glo=0.5)
+    gd, xd, dyd = g.to(DEV), x.to(DEV), dy.to(DEV)
+    cu = torch.tensor(cu_of(lens), device=DEV)
+    for rev in (False, True):
+      h = torch.empty_like(xd)
+      _ops.scan_fwd(gd, xd, h, cu, reverse=rev)
+      check_close(h, oracle_fwd(g, x, lens, rev), dtype, "h (fallback)")
+      dx, dg = torch.empty_like(xd), torch.empty_like(xd)
+      _ops.scan_bwd(dyd, gd, h, dx, dg, cu, causal=not rev)
+      dxr, dgr = oracle.scan_bwd(npf(dy), npf(g), npf(h), cu_of(lens), not rev)
+      check_close(dx, dxr, dtype, "dx (fallback)")
+      check_close(dg, dgr, dtype, "dg (fallback)")
+  finally:
+    lib.asc_set_lookback_spin_limit(prev)
+    _ops.USE_WORKSPACE = prev_ws

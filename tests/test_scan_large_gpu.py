@@ -160,3 +160,85 @@ def test_long_memory_error_vs_sequential_fp32():
   assert np.sqrt(np.mean(e_gpu ** 2)) <= np.sqrt(np.mean(e_seq ** 2))
   # normwise: within rtol 1e-5 of the value scale of each row
   assert (e_gpu.max(1) / np.abs(ref).max(1)).max() < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# few (segment, channel) items: the look-back walk over 1024-element tiles
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(1, [3_000_001]), (3, [1_000_000, 17, 999_983]),
+                                   (1, [4096] * 40 + [7, 1, 2])],
+                         ids=["one-row", "three-rows", "forty-segments"])
+def test_few_items_long_rows(dtype, shape):
+  """One or a few long rows (fewer than 64 items): every tile of 1024
+  elements is its own wave and carries chain through the workspace.  The
+  full result is checked against the oracle and against the
+  workspace-free walk on the same inputs."""
+  C, lens = shape
+  T = sum(lens)
+  gen = _gen(11)
+  g = torch.rand(C, T, device=DEV, generator=gen).mul_(0.05).add_(0.95).to(dtype)
+  x = torch.randn(C, T, device=DEV, generator=gen).to(dtype)
+  dy = torch.rand(C, T, device=DEV, generator=gen).to(dtype)
+  cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), device=DEV)
+  lib = _ops._lib.load()
+  items = (len(lens)) * C
+  assert lib.asc_scan_workspace_bytes(len(lens), C, T, _ops._lib.dtype_code(x), 1) > 0, items
+  for rev in (False, True):
+    h, dx, dg = torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)
+    _ops.scan_fwd(g, x, h, cu, reverse=rev)
+    _ops.scan_bwd(dy, g, h, dx, dg, cu, causal=not rev)
+    torch.cuda.synchronize()
+    _check_fwd_bwd(g, x, dy, h, dx, dg, cu, dtype, list(range(C)), reverse=rev)
+    prev = _ops.USE_WORKSPACE
+    _ops.USE_WORKSPACE = False
+    try:
+      h2, dx2, dg2 = torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)
+      _ops.scan_fwd(g, x, h2, cu, reverse=rev)
+      _ops.scan_bwd(dy, g, h, dx2, dg2, cu, causal=not rev)
+    finally:
+      _ops.USE_WORKSPACE = prev
+    cu_np = cu.cpu().numpy().astype(np.int64)
+    ref_h = oracle.scan_fwd(npf(g), npf(x), cu_np, rev)
+    check_close(h2, ref_h, dtype, "h (workspace-free walk)")
+    # the two walks agree to the output rounding
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    s = max(1.0, float(h.float().square().mean().sqrt()))
+    assert ((h.float() - h2.float()).abs() <= tol * (s + h.float().abs())).all()
+
+
+def test_few_items_bidi_and_fallback():
+  """Both branches in one launch over a single long row, and the
+  bounded-wait fallback forced on every poll (spin limit 0)."""
+  C, lens = 1, [250_000, 3, 250_001]
+  T = sum(lens)
+  gen = _gen(12)
+  gf = torch.rand(C, T, device=DEV, generator=gen).mul_(0.1).add_(0.9)
+  gb = torch.rand(C, T, device=DEV, generator=gen).mul_(0.1).add_(0.9)
+  xf = torch.randn(C, T, device=DEV, generator=gen)
+  xb = torch.randn(C, T, device=DEV, generator=gen)
+  dyf = torch.rand(C, T, device=DEV, generator=gen)
+  dyb = torch.rand(C, T, device=DEV, generator=gen)
+  cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), device=DEV, dtype=torch.int32)
+  cu_np = cu.cpu().numpy().astype(np.int64)
+  lib = _ops._lib.load()
+  for spin in (None, 0):
+    prev = lib.asc_set_lookback_spin_limit(spin) if spin is not None else None
+    try:
+      hf, hb = torch.empty_like(xf), torch.empty_like(xf)
+      _ops.scan_bidi_fwd(gf, xf, gb, xb, hf, hb, cu)
+      d = [torch.empty_like(xf) for _ in range(4)]
+      _ops.scan_bidi_bwd(dyf, dyb, gf, gb, hf, hb, d[0], d[1], d[2], d[3], cu)
+      torch.cuda.synchronize()
+    finally:
+      if prev is not None:
+        lib.asc_set_lookback_spin_limit(prev)
+    check_close(hf, oracle.scan_fwd(npf(gf), npf(xf), cu_np, False), torch.float32, "hf")
+    check_close(hb, oracle.scan_fwd(npf(gb), npf(xb), cu_np, True), torch.float32, "hb")
+    dxf, dgf = oracle.scan_bwd(npf(dyf), npf(gf), npf(hf), cu_np, causal=True)
+    dxb, dgb = oracle.scan_bwd(npf(dyb), npf(gb), npf(hb), cu_np, causal=False)
+    check_close(d[0], dxf, torch.float32, "dx fwd branch")
+    check_close(d[1], dgf, torch.float32, "dg fwd branch")
+    check_close(d[2], dxb, torch.float32, "dx bwd branch")
+    check_close(d[3], dgb, torch.float32, "dg bwd branch")
