@@ -41,8 +41,9 @@ LENS = [
   [1000, 3, 4097],
   [17, 1, 2, 3, 1024, 1025, 250],
   [2 * 4096 + 3, 7],
-  # long segments: walked by the workgroup-cooperative kernels (fp32 from a
-  # mean of 16384 elements, fp16/bf16 from 32768), with short segments mixed in
+  # long segments: without a workspace, fp32 walks them with the
+  # workgroup-cooperative kernels (8 waves from a mean of 8192 elements, 16
+  # from 16384 / 32768); short segments mixed in
   [20000],
   [16384 * 2 + 5],
   [70000, 1, 2, 5000, 100000],

@@ -242,3 +242,48 @@ def test_few_items_bidi_and_fallback():
     check_close(d[1], dgf, torch.float32, "dg fwd branch")
     check_close(d[2], dxb, torch.float32, "dx bwd branch")
     check_close(d[3], dgb, torch.float32, "dg bwd branch")
+
+
+# ---------------------------------------------------------------------------
+# many short segments of mixed lengths: the stretch walk (one wave per chunk
+# of a row, owning the whole segments that start in it)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16],
+                         ids=["f32", "f16", "bf16"])
+def test_mixed_short_segments(dtype):
+  C = 40
+  rng = np.random.default_rng(7)
+  lens = rng.integers(1, 3000, size=300)
+  lens[::37] = 1          # single-element segments
+  lens[5] = 20000         # one long segment among short ones
+  T = int(lens.sum())
+  cu_np = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+  cu = torch.tensor(cu_np, device=DEV)
+  gen = _gen(21)
+  g = torch.rand(C, T, device=DEV, generator=gen).mul_(0.4).add_(0.6).to(dtype)
+  x = torch.randn(C, T, device=DEV, generator=gen).to(dtype)
+  dy = torch.rand(C, T, device=DEV, generator=gen).to(dtype)
+  gb = torch.rand(C, T, device=DEV, generator=gen).mul_(0.4).add_(0.6).to(dtype)
+  xb = torch.randn(C, T, device=DEV, generator=gen).to(dtype)
+  dyb = torch.rand(C, T, device=DEV, generator=gen).to(dtype)
+  for rev in (False, True):
+    h, dx, dg = torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)
+    _ops.scan_fwd(g, x, h, cu, reverse=rev)
+    _ops.scan_bwd(dy, g, h, dx, dg, cu, causal=not rev)
+    torch.cuda.synchronize()
+    _check_fwd_bwd(g, x, dy, h, dx, dg, cu, dtype, list(range(C)), reverse=rev)
+  # both branches in one launch each way
+  hf, hb = torch.empty_like(x), torch.empty_like(x)
+  _ops.scan_bidi_fwd(g, x, gb, xb, hf, hb, cu)
+  d = [torch.empty_like(x) for _ in range(4)]
+  _ops.scan_bidi_bwd(dy, dyb, g, gb, hf, hb, d[0], d[1], d[2], d[3], cu)
+  torch.cuda.synchronize()
+  check_close(hf, oracle.scan_fwd(npf(g), npf(x), cu_np, False), dtype, "hf")
+  check_close(hb, oracle.scan_fwd(npf(gb), npf(xb), cu_np, True), dtype, "hb")
+  dxf, dgf = oracle.scan_bwd(npf(dy), npf(g), npf(hf), cu_np, causal=True)
+  dxb, dgb = oracle.scan_bwd(npf(dyb), npf(gb), npf(hb), cu_np, causal=False)
+  check_close(d[0], dxf, dtype, "dx fwd branch")
+  check_close(d[1], dgf, dtype, "dg fwd branch")
+  check_close(d[2], dxb, dtype, "dx bwd branch")
+  check_close(d[3], dgb, dtype, "dg bwd branch")
