@@ -127,6 +127,70 @@ def scan_bwd(grad: torch.Tensor, gates: torch.Tensor, states: torch.Tensor,
       dt, 1 if causal else 0, _lib.ptr(ws), nb, _lib.stream_of(dev)))
 
 
+def row_constant_stride(grad: torch.Tensor, like: torch.Tensor,
+                        num_channels: int | None = None) -> int | None:
+  """Element stride between rows if `grad` (shaped like `like`) is constant
+  along time in every row -- an expanded tensor with time stride 0, as
+  autograd passes for out.sum() -- else None."""
+  if grad.shape != like.shape or grad.dtype != like.dtype or grad.numel() == 0:
+    return None
+  if grad.device != like.device:
+    return None
+  if grad.dim() == 1:
+    return 0 if grad.stride(0) == 0 else None
+  if grad.dim() != 2 or grad.shape[1] < 2 or grad.stride(1) != 0:
+    return None
+  if grad.stride(0) == 0:
+    return 0
+  if num_channels is not None and int(num_channels) != grad.shape[0]:
+    return None
+  return grad.stride(0)
+
+
+def scan_bwd_rowgrad(grad: torch.Tensor, row_stride: int, gates: torch.Tensor,
+                     states: torch.Tensor, d_tokens: torch.Tensor,
+                     d_gates: torch.Tensor, cu: torch.Tensor, causal: bool,
+                     num_channels: int | None = None) -> None:
+  """Fused backward for a gradient constant along time (one value per row,
+  `row_stride` elements apart, read from grad.data_ptr())."""
+  lib = _lib.load()
+  dev = _lib.require_device(grad, gates, states, d_tokens, d_gates, cu)
+  _check_same(states, gates, d_tokens, d_gates)
+  if grad.dtype != states.dtype:
+    raise TypeError(f"dtype mismatch: {states.dtype} vs {grad.dtype}")
+  dt = _lib.dtype_code(states)
+  cuc = _lib.cu_code(cu)
+  cu = cu.contiguous()
+  S, C, T = _geometry(states, cu, num_channels)
+  with _OnDevice(dev):
+    _lib.check(lib.asc_scan_bwd_rowgrad(
+      grad.data_ptr(), int(row_stride), gates.data_ptr(), states.data_ptr(),
+      d_tokens.data_ptr(), d_gates.data_ptr(), cu.data_ptr(), cuc, S, C, T,
+      dt, 1 if causal else 0, _lib.stream_of(dev)))
+
+
+def scan_bwd_any(grad: torch.Tensor, gates: torch.Tensor, states: torch.Tensor,
+                 d_tokens: torch.Tensor, d_gates: torch.Tensor,
+                 cu: torch.Tensor, causal: bool,
+                 num_channels: int | None = None) -> None:
+  """Backward for any incoming gradient layout: a gradient that is constant
+  along time is read one value per row (no materialised copy) unless the
+  geometry runs the look-back walk; any other layout is made contiguous, as
+  the reference does (scan_eager.py:61)."""
+  rs = row_constant_stride(grad, states, num_channels)
+  if rs is not None:
+    lib = _lib.load()
+    cu_c = cu.contiguous()
+    S, C, T = _geometry(states, cu_c, num_channels)
+    if not USE_WORKSPACE or lib.asc_scan_workspace_bytes(
+        S, C, T, _lib.dtype_code(states), 1) <= 0:
+      scan_bwd_rowgrad(grad, rs, gates, states, d_tokens, d_gates, cu_c,
+                       causal, num_channels)
+      return
+  scan_bwd(grad.contiguous(), gates, states, d_tokens, d_gates, cu, causal,
+           num_channels)
+
+
 def scan_bidi_fwd(gf: torch.Tensor, xf: torch.Tensor, gb: torch.Tensor,
                   xb: torch.Tensor, hf: torch.Tensor, hb: torch.Tensor,
                   cu: torch.Tensor, num_channels: int | None = None) -> None:

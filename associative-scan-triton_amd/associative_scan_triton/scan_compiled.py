@@ -59,12 +59,12 @@ def scan_causal_bwd_op(
   no_channels: int,
   chunk_size: int,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-  """Causal scan backward; returns (d_gates, d_tokens)."""
-  grad = grad.contiguous()
-  d_tokens = torch.empty_like(grad)
+  """Causal scan backward; returns (d_gates, d_tokens).  A gradient that
+  is constant along time is read one value per row, not materialised."""
+  d_tokens = torch.empty_like(states)
   d_gates = torch.empty_like(gates)
-  _ops.scan_bwd(grad, gates, states, d_tokens, d_gates, cu_seqlens,
-                causal=True, num_channels=no_channels)
+  _ops.scan_bwd_any(grad, gates, states, d_tokens, d_gates, cu_seqlens,
+                    causal=True, num_channels=no_channels)
   return d_gates, d_tokens
 
 

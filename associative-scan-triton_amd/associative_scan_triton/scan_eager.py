@@ -46,11 +46,13 @@ class ScanCausal(torch.autograd.Function):
   @staticmethod
   def backward(ctx, grad_output):
     states, gates = ctx.saved_tensors
-    grad_output = grad_output.contiguous()
-    d_tokens = torch.empty_like(grad_output)
+    # A gradient constant along time (out.sum()) is read one value per row
+    # instead of being materialised (the reference's .contiguous(),
+    # scan_eager.py:61); any other layout is made contiguous.
+    d_tokens = torch.empty_like(states)
     d_gates = torch.empty_like(gates)
-    _ops.scan_bwd(grad_output, gates, states, d_tokens, d_gates,
-                  ctx.cu_seqlens, causal=True, num_channels=ctx.grid[2])
+    _ops.scan_bwd_any(grad_output, gates, states, d_tokens, d_gates,
+                      ctx.cu_seqlens, causal=True, num_channels=ctx.grid[2])
     return d_gates, d_tokens, None
 
 

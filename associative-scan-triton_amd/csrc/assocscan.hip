@@ -287,6 +287,18 @@ __device__ inline void load_vec(const char* origin, int64_t vi, bool lane_ok,
   }
 }
 
+// dy of a gradient that is constant along time: value v for the elements
+// inside [P0, P1) (of a valid lane), 0 (the identity) elsewhere.
+template <class IO, bool MASKED>
+__device__ inline void dyc_vec(float v, int64_t vi, bool lane_ok, int64_t P0,
+                               int64_t P1, float* f) {
+  constexpr int V = IO::V;
+  const int64_t pv = vi * V;
+#pragma unroll
+  for (int j = 0; j < V; ++j)
+    f[j] = (!MASKED || (lane_ok && pv + j >= P0 && pv + j < P1)) ? v : 0.0f;
+}
+
 // Stores one vector (memory order); MASKED skips elements outside [P0, P1).
 template <class IO, bool ALN, bool MASKED>
 __device__ inline void store_vec(char* origin, int64_t vi, bool lane_ok,
@@ -600,17 +612,21 @@ __device__ inline void bwd_subtile(const float* g, const float* dy,
   carry_g = readlane(g[mem_idx<V, RB>(V - 1)], kWave - 1);
 }
 
-template <class IO, bool RB, bool ALN, bool MASKED, int NS>
+// DYC: the gradient is the constant dyv along the item (dy is not read).
+template <class IO, bool RB, bool ALN, bool MASKED, int NS, bool DYC>
 __device__ inline void bwd_block(const BwdPtrs& t, const Walk<IO, RB>& w,
                                  int64_t k0, int lane, float& carry,
-                                 float& carry_g) {
+                                 float& carry_g, float dyv) {
   constexpr int V = IO::V;
   float g[NS][V], dy[NS][V], h[NS][V];
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
     const int64_t vi = w.vec(k0 + u, lane);
     const bool ok = !MASKED || w.lane_valid(k0 + u, lane);
-    load_vec<IO, ALN, MASKED>(t.dy, vi, ok, w.P0, w.P1, 0.0f, dy[u]);
+    if (DYC)
+      dyc_vec<IO, MASKED>(dyv, vi, ok, w.P0, w.P1, dy[u]);
+    else
+      load_vec<IO, ALN, MASKED>(t.dy, vi, ok, w.P0, w.P1, 0.0f, dy[u]);
     load_vec<IO, ALN, MASKED>(t.g, vi, ok, w.P0, w.P1, 1.0f, g[u]);
     load_vec<IO, ALN, MASKED>(t.h, vi, ok, w.P0, w.P1, 0.0f, h[u]);
   }
@@ -647,10 +663,10 @@ __device__ inline float bwd_halo(const BwdPtrs& t, const Walk<IO, RB>& w,
 }
 
 // Interior sub-tiles of the backward, software-pipelined like fwd_fast.
-template <class IO, bool RB, int U>
+template <class IO, bool RB, int U, bool DYC>
 __device__ inline void bwd_fast(const BwdPtrs& t, const Walk<IO, RB>& w,
                                 int64_t k, int64_t kend, int lane,
-                                float& carry, float& carry_g) {
+                                float& carry, float& carry_g, float dyv) {
   constexpr int V = IO::V;
   constexpr int STEP = RB ? -kWave * 16 : kWave * 16;
   const uint32_t lo = lane_off<RB>(lane);
@@ -664,7 +680,7 @@ __device__ inline void bwd_fast(const BwdPtrs& t, const Walk<IO, RB>& w,
     const char* hp = t.h + b + lo;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      y[u] = ld16(yp + u * STEP);
+      if (!DYC) y[u] = ld16(yp + u * STEP);
       g[u] = ld16(gp + u * STEP);
       h[u] = ld16(hp + u * STEP);
     }
@@ -681,7 +697,12 @@ __device__ inline void bwd_fast(const BwdPtrs& t, const Walk<IO, RB>& w,
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float yf[V], gf[V], dx[V], dg[V];
-      IO::unpack(y[u], yf);
+      if (DYC) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) yf[j] = dyv;
+      } else {
+        IO::unpack(y[u], yf);
+      }
       IO::unpack(g[u], gf);
       const float hin =
           (u + 1 < U) ? readlane(hf[u + 1][mem_idx<V, RB>(0)], 0) : halo;
@@ -706,27 +727,28 @@ __device__ inline void bwd_fast(const BwdPtrs& t, const Walk<IO, RB>& w,
   }
 }
 
-template <class IO, bool RB, bool ALN>
-__device__ void bwd_item(const BwdPtrs& t, int64_t P0, int64_t P1, int lane) {
+template <class IO, bool RB, bool ALN, bool DYC>
+__device__ void bwd_item(const BwdPtrs& t, int64_t P0, int64_t P1, int lane,
+                         float dyv) {
   constexpr int U = ASC_BWD_UNROLL;
   const Walk<IO, RB> w(P0, P1);
   float carry = 0.0f, carry_g = 1.0f;
-  bwd_block<IO, RB, ALN, true, 1>(t, w, 0, lane, carry, carry_g);
+  bwd_block<IO, RB, ALN, true, 1, DYC>(t, w, 0, lane, carry, carry_g, dyv);
   int64_t k = 1;
   if (ALN) {
     const int64_t nfull = (w.kfast - 1) / U * U;
     if (nfull > 0) {
-      bwd_fast<IO, RB, U>(t, w, 1, 1 + nfull, lane, carry, carry_g);
+      bwd_fast<IO, RB, U, DYC>(t, w, 1, 1 + nfull, lane, carry, carry_g, dyv);
       k = 1 + nfull;
     }
   } else {
     for (; k + U <= w.kfast; k += U)
-      bwd_block<IO, RB, ALN, false, U>(t, w, k, lane, carry, carry_g);
+      bwd_block<IO, RB, ALN, false, U, DYC>(t, w, k, lane, carry, carry_g, dyv);
   }
   for (; k < w.kfast; ++k)
-    bwd_block<IO, RB, ALN, false, 1>(t, w, k, lane, carry, carry_g);
+    bwd_block<IO, RB, ALN, false, 1, DYC>(t, w, k, lane, carry, carry_g, dyv);
   for (; k < w.nsub; ++k)
-    bwd_block<IO, RB, ALN, true, 1>(t, w, k, lane, carry, carry_g);
+    bwd_block<IO, RB, ALN, true, 1, DYC>(t, w, k, lane, carry, carry_g, dyv);
 }
 
 // ---------------------------------------------------------------------------
@@ -855,9 +877,9 @@ __device__ inline float bwd_gate_before(const BwdPtrs& t,
   return (pp >= w.P0 && pp < w.P1) ? IO::load1(t.g + pp * IO::ES) : 1.0f;
 }
 
-template <class IO, bool RB, bool ALN, int NW>
+template <class IO, bool RB, bool ALN, int NW, bool DYC>
 __device__ void bwd_item_wg(const BwdPtrs& t, int64_t P0, int64_t P1,
-                            int lane, int wv, float2* agg) {
+                            int lane, int wv, float2* agg, float dyv) {
   constexpr int V = IO::V;
   constexpr int TS = NW * kUW;
   constexpr int jl = mem_idx<V, RB>(V - 1);
@@ -873,7 +895,15 @@ __device__ void bwd_item_wg(const BwdPtrs& t, int64_t P0, int64_t P1,
     const int64_t k0 = it * TS + wv * kUW;
 #pragma unroll
     for (int u = 0; u < kUW; ++u) {
-      load_sub<IO, RB, ALN>(t.dy, w, k0 + u, lane, 0.0f, y[u]);
+      if (DYC) {
+        if (interior(w, k0 + u))
+          dyc_vec<IO, false>(dyv, 0, true, 0, 0, y[u]);
+        else
+          dyc_vec<IO, true>(dyv, w.vec(k0 + u, lane), w.lane_valid(k0 + u, lane),
+                            w.P0, w.P1, y[u]);
+      } else {
+        load_sub<IO, RB, ALN>(t.dy, w, k0 + u, lane, 0.0f, y[u]);
+      }
       load_sub<IO, RB, ALN>(t.g, w, k0 + u, lane, 1.0f, g[u]);
       load_sub<IO, RB, ALN>(t.h, w, k0 + u, lane, 0.0f, h[u]);
     }
@@ -965,7 +995,7 @@ __device__ inline int64_t cu_at(const Geometry& geo, int64_t i) {
 // otherwise they are the same segment of neighbouring channels.
 template <bool SEG_MAJOR>
 __device__ inline bool item_range(const Geometry& geo, int64_t w, int& br,
-                                  int64_t& P0, int64_t& P1) {
+                                  int64_t& P0, int64_t& P1, int64_t& row) {
   br = w >= geo.items ? 1 : 0;
   const int64_t r = w - br * geo.items;
   int64_t s, c;
@@ -982,6 +1012,7 @@ __device__ inline bool item_range(const Geometry& geo, int64_t w, int& br,
   const int64_t base = c * geo.T + geo.phase;
   P0 = base + t0;
   P1 = base + t1;
+  row = c;
   return P1 > P0;
 }
 
@@ -1002,8 +1033,8 @@ __global__ void __launch_bounds__(kWPB* kWave) k_scan_fwd(FwdParams p) {
   for (int64_t w = static_cast<int64_t>(blockIdx.x) * kWPB + wave_id(); w < W;
        w += stride) {
     int br;
-    int64_t P0, P1;
-    if (!item_range<true>(p.geo, w, br, P0, P1)) continue;
+    int64_t P0, P1, row;
+    if (!item_range<true>(p.geo, w, br, P0, P1, row)) continue;
     const FwdPtrs& t = p.br[br];
     if (DIRS == 1 || (DIRS == 3 && br == 0))
       fwd_item<IO, false, ALN, WA>(t, P0, P1, lane);
@@ -1015,12 +1046,20 @@ __global__ void __launch_bounds__(kWPB* kWave) k_scan_fwd(FwdParams p) {
 struct BwdParams {
   Geometry geo;
   BwdPtrs br[2];
+  int64_t dy_rs;  // DYC: element stride between rows of the gradient
 };
+
+// DYC: the gradient of row c is the one value dy[c * dy_rs] (unshifted dy).
+template <class IO, bool DYC>
+__device__ inline float dyc_value(const BwdParams& p, int br, int64_t row) {
+  if (!DYC) return 0.0f;
+  return IO::load1(p.br[br].dy + row * p.dy_rs * IO::ES);
+}
 
 // DIRS refers to the forward scan being differentiated: 1 = causal forward
 // (adjoint runs in reverse), 2 = reverse forward (adjoint runs forward),
 // 3 = branch 0 causal / branch 1 reverse.
-template <class IO, int DIRS, bool ALN>
+template <class IO, int DIRS, bool ALN, bool DYC>
 __global__ void __launch_bounds__(kWPB* kWave) k_scan_bwd(BwdParams p) {
   const int lane = threadIdx.x % kWave;
   const int64_t W = p.geo.items * p.geo.nbranch;
@@ -1028,13 +1067,14 @@ __global__ void __launch_bounds__(kWPB* kWave) k_scan_bwd(BwdParams p) {
   for (int64_t w = static_cast<int64_t>(blockIdx.x) * kWPB + wave_id(); w < W;
        w += stride) {
     int br;
-    int64_t P0, P1;
-    if (!item_range<true>(p.geo, w, br, P0, P1)) continue;
+    int64_t P0, P1, row;
+    if (!item_range<true>(p.geo, w, br, P0, P1, row)) continue;
     const BwdPtrs& t = p.br[br];
+    const float dyv = dyc_value<IO, DYC>(p, br, row);
     if (DIRS == 1 || (DIRS == 3 && br == 0))
-      bwd_item<IO, true, ALN>(t, P0, P1, lane);
+      bwd_item<IO, true, ALN, DYC>(t, P0, P1, lane, dyv);
     else
-      bwd_item<IO, false, ALN>(t, P0, P1, lane);
+      bwd_item<IO, false, ALN, DYC>(t, P0, P1, lane, dyv);
   }
 }
 
@@ -1047,8 +1087,8 @@ __global__ void __launch_bounds__(NW* kWave) k_scan_fwd_wg(FwdParams p) {
   const int64_t W = p.geo.items * p.geo.nbranch;
   for (int64_t item = blockIdx.x; item < W; item += gridDim.x) {
     int br;
-    int64_t P0, P1;
-    if (!item_range<false>(p.geo, item, br, P0, P1)) continue;
+    int64_t P0, P1, row;
+    if (!item_range<false>(p.geo, item, br, P0, P1, row)) continue;
     const FwdPtrs& t = p.br[br];
     if (DIRS == 1 || (DIRS == 3 && br == 0))
       fwd_item_wg<IO, false, ALN, NW>(t, P0, P1, lane, wv, agg);
@@ -1058,7 +1098,7 @@ __global__ void __launch_bounds__(NW* kWave) k_scan_fwd_wg(FwdParams p) {
   }
 }
 
-template <class IO, int DIRS, bool ALN, int NW>
+template <class IO, int DIRS, bool ALN, int NW, bool DYC>
 __global__ void __launch_bounds__(NW* kWave) k_scan_bwd_wg(BwdParams p) {
   __shared__ float2 agg[2 * NW];
   const int lane = threadIdx.x % kWave;
@@ -1066,13 +1106,14 @@ __global__ void __launch_bounds__(NW* kWave) k_scan_bwd_wg(BwdParams p) {
   const int64_t W = p.geo.items * p.geo.nbranch;
   for (int64_t item = blockIdx.x; item < W; item += gridDim.x) {
     int br;
-    int64_t P0, P1;
-    if (!item_range<false>(p.geo, item, br, P0, P1)) continue;
+    int64_t P0, P1, row;
+    if (!item_range<false>(p.geo, item, br, P0, P1, row)) continue;
     const BwdPtrs& t = p.br[br];
+    const float dyv = dyc_value<IO, DYC>(p, br, row);
     if (DIRS == 1 || (DIRS == 3 && br == 0))
-      bwd_item_wg<IO, true, ALN, NW>(t, P0, P1, lane, wv, agg);
+      bwd_item_wg<IO, true, ALN, NW, DYC>(t, P0, P1, lane, wv, agg, dyv);
     else
-      bwd_item_wg<IO, false, ALN, NW>(t, P0, P1, lane, wv, agg);
+      bwd_item_wg<IO, false, ALN, NW, DYC>(t, P0, P1, lane, wv, agg, dyv);
     __syncthreads();
   }
 }
@@ -2162,11 +2203,15 @@ const void* pick_fwd_wg(int dirs, bool aln) {
 }
 
 template <class IO, int NW>
-const void* pick_bwd_wg(int dirs, bool aln) {
-#define ASC_B(D, A) reinterpret_cast<const void*>(&k_scan_bwd_wg<IO, D, A, NW>)
-  if (dirs == 1) return aln ? ASC_B(1, true) : ASC_B(1, false);
-  if (dirs == 2) return aln ? ASC_B(2, true) : ASC_B(2, false);
-  return aln ? ASC_B(3, true) : ASC_B(3, false);
+const void* pick_bwd_wg(int dirs, bool aln, bool dyc) {
+#define ASC_B(D, A, Y) reinterpret_cast<const void*>(&k_scan_bwd_wg<IO, D, A, NW, Y>)
+  if (dyc) {  // single-branch calls only
+    if (dirs == 1) return aln ? ASC_B(1, true, true) : ASC_B(1, false, true);
+    return aln ? ASC_B(2, true, true) : ASC_B(2, false, true);
+  }
+  if (dirs == 1) return aln ? ASC_B(1, true, false) : ASC_B(1, false, false);
+  if (dirs == 2) return aln ? ASC_B(2, true, false) : ASC_B(2, false, false);
+  return aln ? ASC_B(3, true, false) : ASC_B(3, false, false);
 #undef ASC_B
 }
 
@@ -2176,8 +2221,9 @@ const void* pick_fwd_wg(int nw, int dirs, bool aln) {
 }
 
 template <class IO>
-const void* pick_bwd_wg(int nw, int dirs, bool aln) {
-  return nw == 16 ? pick_bwd_wg<IO, 16>(dirs, aln) : pick_bwd_wg<IO, 8>(dirs, aln);
+const void* pick_bwd_wg(int nw, int dirs, bool aln, bool dyc) {
+  return nw == 16 ? pick_bwd_wg<IO, 16>(dirs, aln, dyc)
+                  : pick_bwd_wg<IO, 8>(dirs, aln, dyc);
 }
 
 template <class IO>
@@ -2214,11 +2260,15 @@ const void* pick_fwd(int dirs, bool aln, bool wa) {
 }
 
 template <class IO>
-const void* pick_bwd(int dirs, bool aln) {
-#define ASC_B(D, A) reinterpret_cast<const void*>(&k_scan_bwd<IO, D, A>)
-  if (dirs == 1) return aln ? ASC_B(1, true) : ASC_B(1, false);
-  if (dirs == 2) return aln ? ASC_B(2, true) : ASC_B(2, false);
-  return aln ? ASC_B(3, true) : ASC_B(3, false);
+const void* pick_bwd(int dirs, bool aln, bool dyc) {
+#define ASC_B(D, A, Y) reinterpret_cast<const void*>(&k_scan_bwd<IO, D, A, Y>)
+  if (dyc) {  // single-branch calls only
+    if (dirs == 1) return aln ? ASC_B(1, true, true) : ASC_B(1, false, true);
+    return aln ? ASC_B(2, true, true) : ASC_B(2, false, true);
+  }
+  if (dirs == 1) return aln ? ASC_B(1, true, false) : ASC_B(1, false, false);
+  if (dirs == 2) return aln ? ASC_B(2, true, false) : ASC_B(2, false, false);
+  return aln ? ASC_B(3, true, false) : ASC_B(3, false, false);
 #undef ASC_B
 }
 
@@ -2295,27 +2345,35 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
   return launch(fn, (items + kWPB - 1) / kWPB, kWPB, p, stream);
 }
 
+// dyc: dy[0] holds one gradient value per row (element stride dy_rs between
+// rows) that is constant along time; single-branch calls only.
 int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
             void* const* dx, void* const* dg, int nbranch, int dirs,
             const void* cu, int cu_dtype, int64_t S, int64_t C, int64_t T,
-            int dtype, void* ws, int64_t ws_bytes, void* stream) {
+            int dtype, void* ws, int64_t ws_bytes, void* stream,
+            bool dyc = false, int64_t dy_rs = 0) {
   int st = check_geometry(cu, cu_dtype, S, C, T, dtype);
   if (st) return st;
   for (int b = 0; b < nbranch; ++b)
     if (!dy[b] || !g[b] || !h[b] || !dx[b] || !dg[b]) return ASC_E_NULL;
   const int es = elem_size(dtype);
   const int v = 16 / es;
+  if (dyc && (nbranch != 1 || dy_rs < 0)) return ASC_E_ARG;
   const void* all[10];
   int n = 0;
   for (int b = 0; b < nbranch; ++b) {
-    all[n++] = dy[b];
     all[n++] = g[b];
     all[n++] = h[b];
     all[n++] = dx[b];
     all[n++] = dg[b];
   }
   if ((st = check_ptrs(all, n, es))) return st;
+  if ((st = check_ptrs(dy, nbranch, es))) return st;
   if (S == 0 || C == 0 || T == 0) return ASC_OK;
+  // the per-row gradient of dyc is read by scalar loads: its alignment does
+  // not enter the phase
+  if (!dyc)
+    for (int b = 0; b < nbranch; ++b) all[n++] = dy[b];
   const int ph = common_phase(all, n, es, v);
   const bool aln = ph >= 0;
   BwdParams p{};
@@ -2323,14 +2381,15 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
                    aln ? ph : 0};
   const int64_t shift = static_cast<int64_t>(p.geo.phase) * es;
   for (int b = 0; b < nbranch; ++b) {
-    p.br[b].dy = static_cast<const char*>(dy[b]) - shift;
+    p.br[b].dy = static_cast<const char*>(dy[b]) - (dyc ? 0 : shift);
     p.br[b].g = static_cast<const char*>(g[b]) - shift;
     p.br[b].h = static_cast<const char*>(h[b]) - shift;
     p.br[b].dx = static_cast<char*>(dx[b]) - shift;
     p.br[b].dg = static_cast<char*>(dg[b]) - shift;
   }
+  p.dy_rs = dy_rs;
   const int64_t items = p.geo.items * nbranch;
-  if (ws && reinterpret_cast<uintptr_t>(ws) % 32 == 0 &&
+  if (!dyc && ws && reinterpret_cast<uintptr_t>(ws) % 32 == 0 &&
       lb_use(S, C, T, nbranch)) {
     LbBwdParams q{};
     q.geo = LbGeo{cu, cu_dtype == ASC_CU_I64, S, C, T, C * T, p.geo.phase,
@@ -2357,14 +2416,14 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
     const void* fn = nullptr;
     // pick_walk returns workgroup walks for fp32 only
     if (dtype != ASC_F32) return ASC_E_ARG;
-    fn = pick_bwd_wg<IoF32>(nw, dirs, aln);
+    fn = pick_bwd_wg<IoF32>(nw, dirs, aln, dyc);
     return launch(fn, items, nw, p, stream);
   }
   const void* fn = nullptr;
   switch (dtype) {
-    case ASC_F32: fn = pick_bwd<IoF32>(dirs, aln); break;
-    case ASC_F16: fn = pick_bwd<IoF16>(dirs, aln); break;
-    default: fn = pick_bwd<IoBF16>(dirs, aln); break;
+    case ASC_F32: fn = pick_bwd<IoF32>(dirs, aln, dyc); break;
+    case ASC_F16: fn = pick_bwd<IoF16>(dirs, aln, dyc); break;
+    default: fn = pick_bwd<IoBF16>(dirs, aln, dyc); break;
   }
   return launch(fn, (items + kWPB - 1) / kWPB, kWPB, p, stream);
 }
@@ -2433,6 +2492,23 @@ int asc_scan_bwd(const void* grad, const void* gates, const void* states,
   return run_bwd(dy, g, h, dx, dg, 1, causal ? 1 : 2, cu_seqlens, cu_dtype,
                  num_seq, num_channels, seq_stride, dtype, workspace,
                  workspace_bytes, stream);
+}
+
+int asc_scan_bwd_rowgrad(const void* grad_rows, int64_t grad_row_stride,
+                         const void* gates, const void* states, void* d_tokens,
+                         void* d_gates, const void* cu_seqlens, int cu_dtype,
+                         int64_t num_seq, int64_t num_channels,
+                         int64_t seq_stride, int dtype, int causal,
+                         void* stream) {
+  const void* dy[1] = {grad_rows};
+  const void* g[1] = {gates};
+  const void* h[1] = {states};
+  void* dx[1] = {d_tokens};
+  void* dg[1] = {d_gates};
+  if (grad_row_stride < 0) return ASC_E_ARG;
+  return run_bwd(dy, g, h, dx, dg, 1, causal ? 1 : 2, cu_seqlens, cu_dtype,
+                 num_seq, num_channels, seq_stride, dtype, nullptr, 0, stream,
+                 true, grad_row_stride);
 }
 
 int asc_scan_bidi_fwd(const void* gates_fwd, const void* tokens_fwd,

@@ -132,6 +132,26 @@ int asc_scan_bwd(const void* grad, const void* gates, const void* states,
                  int64_t workspace_bytes, void* stream);
 
 /*
+ * The same fused backward for a gradient that is constant along time in
+ * every row: grad[c, t] = grad_rows[c * grad_row_stride] for all t
+ * (grad_row_stride = 0: one value for the whole tensor).  This is the
+ * gradient of out.sum() (or of any loss that reduces over time first), which
+ * PyTorch hands over as a stride-0 expanded tensor.  The kernels read one
+ * value per row instead of a [C, T] tensor: 4 of the 5 tensors' traffic, and
+ * no materialised copy.  Runs the workspace-free walks.
+ *
+ * Replaces: scan_eager.py:58-63 (grad_output.contiguous() followed by
+ *   backward_scan_fused_full) and scan_compiled.py:158-166 when the incoming
+ *   gradient is such an expanded tensor.
+ */
+int asc_scan_bwd_rowgrad(const void* grad_rows, int64_t grad_row_stride,
+                         const void* gates, const void* states, void* d_tokens,
+                         void* d_gates, const void* cu_seqlens, int cu_dtype,
+                         int64_t num_seq, int64_t num_channels,
+                         int64_t seq_stride, int dtype, int causal,
+                         void* stream);
+
+/*
  * Both branches of the bidirectional scan in ONE launch: a causal scan of
  * (gates_fwd, tokens_fwd) into h_fwd and a reverse scan of
  * (gates_bwd, tokens_bwd) into h_bwd.

@@ -97,3 +97,21 @@ def test_workspace_bytes():
 def test_error_is_raised_with_message():
   with pytest.raises(_lib.AscError, match="NULL"):
     _lib.check(-1)
+
+
+def test_rowgrad_validation_codes():
+  lib = _lib.load()
+  args = dict(grad=8, rs=0, gates=8, states=8, dx=8, dg=8, cu=8, cu_dtype=0,
+              S=1, C=1, T=4, dtype=0, causal=1, stream=None)
+
+  def call(**kw):
+    a = dict(args)
+    a.update(kw)
+    return lib.asc_scan_bwd_rowgrad(*a.values())
+
+  assert call(grad=None) == -1
+  assert call(dg=None) == -1
+  assert call(rs=-1) == -5
+  assert call(dtype=5) == -2
+  assert call(grad=6) == -4       # fp32 gradient not 4-byte aligned
+  assert call(S=0) == 0           # empty: nothing launched

@@ -104,3 +104,21 @@ def test_op_on_tensors():
   f, x = ast.op(fl, xl, fr, xr)
   assert torch.equal(f, fr * fl)
   assert torch.equal(x, fr * xl + xr)
+
+
+def test_row_constant_stride_detection():
+  """Which incoming gradient layouts take the one-value-per-row backward."""
+  from associative_scan_triton._ops import row_constant_stride
+  like = torch.empty(6, 50)
+  assert row_constant_stride(torch.ones(()).expand(6, 50), like) == 0
+  assert row_constant_stride(torch.ones(6, 1).expand(6, 50), like) == 1
+  w = torch.ones(6, 3)[:, 1:2].expand(6, 50)       # rows 3 elements apart
+  assert row_constant_stride(w, like) == 3
+  assert row_constant_stride(w, like, num_channels=6) == 3
+  assert row_constant_stride(w, like, num_channels=3) is None  # flat addressing
+  assert row_constant_stride(torch.ones(6, 50), like) is None   # dense
+  assert row_constant_stride(torch.ones(50).expand(6, 50), like) is None
+  assert row_constant_stride(torch.ones(()).expand(6, 50).double(), like) is None
+  flat = torch.empty(300)
+  assert row_constant_stride(torch.ones(()).expand(300), flat) == 0
+  assert row_constant_stride(torch.ones(300), flat) is None

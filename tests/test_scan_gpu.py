@@ -606,3 +606,118 @@ def test_lookback_fallback_path(lens, dtype):
   finally:
     lib.asc_set_lookback_spin_limit(prev)
     _ops.USE_WORKSPACE = prev_ws
+
+
+# ---------------------------------------------------------------------------
+# gradients constant along time (out.sum().backward())
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("lens,C", [([3000, 17, 5000], 80), ([70000, 40000], 40),
+                                    ([100, 200], 2)],
+                         ids=["short", "long", "few-items"])
+@pytest.mark.parametrize("compiled", [False, True], ids=["eager", "compiled"])
+def test_time_constant_gradient(dtype, lens, C, compiled):
+  """out.sum() and (out.sum(-1) * w).sum() hand the backward an expanded
+  gradient (time stride 0); reading one value per row must give the same
+  bits as the materialised gradient, and match the oracle."""
+  fn = ast.scan_causal_compiled if compiled else ast.scan_causal
+  g, x = make(lens, C, dtype, glo=0.5)
+  args = grid_args(lens, C)
+  w = torch.rand(C, generator=torch.Generator().manual_seed(3)).to(dtype).to(DEV)
+
+  def grads(loss_of):
+    gd = g.to(DEV).requires_grad_(True)
+    xd = x.to(DEV).requires_grad_(True)
+    y = fn(gd, xd, args)
+    loss_of(y)
+    return y.detach(), gd.grad, xd.grad
+
+  T = sum(lens)
+  for loss_of, dense in (
+      (lambda y: y.sum().backward(), torch.ones(C, T, dtype=dtype, device=DEV)),
+      (lambda y: (y.sum(-1) * w).sum().backward(),
+       w[:, None].expand(C, T).contiguous())):
+    y1, dg1, dx1 = grads(loss_of)
+    y2, dg2, dx2 = grads(lambda y: y.backward(dense))
+    assert torch.equal(dx1, dx2) and torch.equal(dg1, dg2)
+    dx_ref, dg_ref = oracle_bwd(dense.cpu(), g, npf(y1), lens)
+    check_close(dx1, dx_ref, dtype, "dx")
+    check_close(dg1, dg_ref, dtype, "dg")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "anticausal"])
+def test_rowgrad_entry_point(dtype, causal):
+  """asc_scan_bwd_rowgrad directly: one value per row, rows 3 elements
+  apart, every walk (workgroup for long fp32 segments, one wave per item)."""
+  from associative_scan_triton import _ops
+  for lens, C in (([70000, 5, 33000], 70), ([900, 1, 2, 4096], 100)):
+    g, h = make(lens, C, dtype, n=2, glo=0.5)
+    rows = torch.randn(C, 3, generator=torch.Generator().manual_seed(5)).to(dtype)
+    T = sum(lens)
+    dx = torch.empty(C, T, dtype=dtype, device=DEV)
+    dg = torch.empty_like(dx)
+    cu = torch.tensor(cu_of(lens), device=DEV)
+    rd = rows.to(DEV)
+    _ops.scan_bwd_rowgrad(rd[:, 1], 3, g.to(DEV), h.to(DEV), dx, dg, cu, causal)
+    dy = rows[:, 1:2].expand(C, T)
+    dx_ref, dg_ref = oracle.scan_bwd(npf(dy), npf(g), npf(h), cu_of(lens), causal)
+    check_close(dx, dx_ref, dtype, "dx")
+    check_close(dg, dg_ref, dtype, "dg")
+
+
+# ---------------------------------------------------------------------------
+# HIP graph capture
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("C,lens", [(2, [5000, 3000]), (64, [700, 300])],
+                         ids=["lookback", "per-item"])
+def test_graph_capture_replay(C, lens):
+  """Forward + backward captured in one graph (the look-back walk clears its
+  workspace with a kernel, not a memset) and replayed with fresh inputs and
+  eager launches in between; every replay matches the oracle, and the
+  deterministic per-item walks match the eager launch bit for bit."""
+  from associative_scan_triton import _ops
+  T = sum(lens)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  g = torch.empty(C, T, device=DEV)
+  x, dy = torch.empty_like(g), torch.empty_like(g)
+  h, dx, dg = torch.empty_like(g), torch.empty_like(g), torch.empty_like(g)
+
+  def step():
+    _ops.scan_fwd(g, x, h, cu, reverse=False)
+    _ops.scan_bwd(dy, g, h, dx, dg, cu, causal=True)
+
+  gen = torch.Generator(device=DEV).manual_seed(9)
+
+  def fresh():
+    g.copy_(torch.rand(C, T, device=DEV, generator=gen).mul_(0.5).add_(0.5))
+    x.copy_(torch.randn(C, T, device=DEV, generator=gen))
+    dy.copy_(torch.rand(C, T, device=DEV, generator=gen))
+
+  fresh()
+  side = torch.cuda.Stream()
+  side.wait_stream(torch.cuda.current_stream())
+  with torch.cuda.stream(side):
+    step()
+  torch.cuda.current_stream().wait_stream(side)
+  graph = torch.cuda.CUDAGraph()
+  with torch.cuda.graph(graph):
+    step()
+  lookback = _ops._lib.load().asc_scan_workspace_bytes(len(lens), C, T, 0, 1) > 0
+  assert lookback == (C == 2)
+  for _ in range(4):
+    fresh()
+    graph.replay()
+    torch.cuda.synchronize()
+    got = [t.clone() for t in (h, dx, dg)]
+    gs, xs, dys = g.cpu(), x.cpu(), dy.cpu()
+    check_close(got[0], oracle_fwd(gs, xs, lens), torch.float32, "h (replay)")
+    dx_ref, dg_ref = oracle.scan_bwd(npf(dys), npf(gs), npf(got[0]), cu_of(lens), True)
+    check_close(got[1], dx_ref, torch.float32, "dx (replay)")
+    check_close(got[2], dg_ref, torch.float32, "dg (replay)")
+    step()
+    torch.cuda.synchronize()
+    if not lookback:
+      assert all(torch.equal(a, b) for a, b in zip(got, (h, dx, dg)))
