@@ -63,6 +63,8 @@ def parse():
   p.add_argument("--config", default="cfg5", choices=sorted(CONFIGS))
   p.add_argument("--no-cpu-baseline", action="store_true")
   p.add_argument("--no-check", action="store_true")
+  p.add_argument("--no-api", action="store_true",
+                 help="skip the API-level (autograd, out.sum()) timing")
   p.add_argument("--profile-copy", action="store_true",
                  help="also launch one plain device copy of one tensor "
                       "(rocprof byte-counter calibration)")
@@ -245,6 +247,44 @@ def main():
            "ms_per_step_equiv": round(cpu_s * 1e3 * N / n_s, 1)}
     log(f"[bench] cpu baseline: {cpu}")
 
+  # ---- API level: the public autograd function, loss = out.sum() ----
+  # (the reference's API benchmark pattern; includes the autograd
+  # bookkeeping, output allocation and, for the sum, the stride-0 gradient)
+  api = None
+  if with_bwd and not a.no_api:
+    import associative_scan_triton as ast
+    args = {"cu_seqlens": cu, "chunk_size": 128,
+            "grid": ast.get_grid(B + 1, int((cu[1:] - cu[:-1]).max()), 128, C)}
+    leaves = [t.detach().requires_grad_(True) for t in (g + x)]
+
+    def api_step():
+      for t in leaves:
+        t.grad = None
+      if kind == "bidi":
+        yf, yb = ast.scan_bidirectional_branched(leaves[0], leaves[2],
+                                                 leaves[1], leaves[3], args)
+        (yf.sum() + yb.sum()).backward()
+      else:
+        ast.scan_causal(leaves[0], leaves[1], args).sum().backward()
+
+    for _ in range(a.warmup):
+      api_step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(a.steps):
+      api_step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    api_ms = e0.elapsed_time(e1) / a.steps
+    api = {"ms_per_step": round(api_ms, 4),
+           "what": ("scan_bidirectional_branched + (out_f.sum() + out_b.sum())"
+                    ".backward()" if kind == "bidi" else
+                    "scan_causal + out.sum().backward()"),
+           "GBs_algorithmic": round(step_bytes / (api_ms * 1e-3) / 1e9, 2)}
+    del leaves
+    log(f"[bench] api level: {api}")
+
   traffic = None
   tf = ROOT / "profiles" / f"traffic_{a.config}.json"
   if tf.exists():
@@ -276,6 +316,7 @@ def main():
                  "traffic": traffic,
                  "algorithmic_bytes": dom_bytes},
     "cpu_baseline": cpu,
+    "api": api,
     "check": check,
   }
   print(json.dumps(out), flush=True)
