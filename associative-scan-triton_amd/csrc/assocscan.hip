@@ -895,24 +895,30 @@ __device__ void bwd_item_wg(const BwdPtrs& t, int64_t P0, int64_t P1,
     const int64_t k0 = it * TS + wv * kUW;
 #pragma unroll
     for (int u = 0; u < kUW; ++u) {
-      if (DYC) {
-        if (interior(w, k0 + u))
-          dyc_vec<IO, false>(dyv, 0, true, 0, 0, y[u]);
-        else
-          dyc_vec<IO, true>(dyv, w.vec(k0 + u, lane), w.lane_valid(k0 + u, lane),
-                            w.P0, w.P1, y[u]);
-      } else {
-        load_sub<IO, RB, ALN>(t.dy, w, k0 + u, lane, 0.0f, y[u]);
-      }
+      if (!DYC) load_sub<IO, RB, ALN>(t.dy, w, k0 + u, lane, 0.0f, y[u]);
       load_sub<IO, RB, ALN>(t.g, w, k0 + u, lane, 1.0f, g[u]);
       load_sub<IO, RB, ALN>(t.h, w, k0 + u, lane, 0.0f, h[u]);
     }
     gp = bwd_gate_before(t, w, k0);
     hn = bwd_halo(t, w, k0, kUW);
   };
-  auto step = [&](const float(&y)[kUW][V], const float(&g)[kUW][V],
+  auto step = [&](const float(&yl)[kUW][V], const float(&g)[kUW][V],
                   const float(&h)[kUW][V], float gp, float hn, int64_t it) {
     const int64_t k0 = it * TS + wv * kUW;
+    // DYC: dy is built here from the row's value, not carried in the
+    // ping-pong buffers
+    float yc[kUW][V];
+    if (DYC) {
+#pragma unroll
+      for (int u = 0; u < kUW; ++u) {
+        if (interior(w, k0 + u))
+          dyc_vec<IO, false>(dyv, 0, true, 0, 0, yc[u]);
+        else
+          dyc_vec<IO, true>(dyv, w.vec(k0 + u, lane), w.lane_valid(k0 + u, lane),
+                            w.P0, w.P1, yc[u]);
+      }
+    }
+    const float(&y)[kUW][V] = DYC ? yc : yl;
     SubScan sc[kUW];
     float gprv[kUW];
     float wa = 1.0f, wx = 0.0f, cg = gp;
@@ -1079,8 +1085,11 @@ __global__ void __launch_bounds__(kWPB* kWave) k_scan_bwd(BwdParams p) {
 }
 
 // Workgroup-cooperative kernels: one item per workgroup of NW waves.
+#ifndef ASC_WG_ATTR
+#define ASC_WG_ATTR
+#endif
 template <class IO, int DIRS, bool ALN, int NW>
-__global__ void __launch_bounds__(NW* kWave) k_scan_fwd_wg(FwdParams p) {
+__global__ void __launch_bounds__(NW* kWave) ASC_WG_ATTR k_scan_fwd_wg(FwdParams p) {
   __shared__ float2 agg[2 * NW];
   const int lane = threadIdx.x % kWave;
   const int wv = wave_id();
@@ -1099,7 +1108,7 @@ __global__ void __launch_bounds__(NW* kWave) k_scan_fwd_wg(FwdParams p) {
 }
 
 template <class IO, int DIRS, bool ALN, int NW, bool DYC>
-__global__ void __launch_bounds__(NW* kWave) k_scan_bwd_wg(BwdParams p) {
+__global__ void __launch_bounds__(NW* kWave) ASC_WG_ATTR k_scan_bwd_wg(BwdParams p) {
   __shared__ float2 agg[2 * NW];
   const int lane = threadIdx.x % kWave;
   const int wv = wave_id();
