@@ -510,6 +510,57 @@ def test_custom_ops_opcheck():
                         (xd.detach(), cu, 0.0, True))
 
 
+def test_custom_ops_opcheck_backward():
+  """The backward ops too, with a dense and a time-constant (stride-0)
+  incoming gradient."""
+  lens = [40, 9]
+  C = 3
+  g, h, dy = make(lens, C, n=3)
+  cu = torch.tensor(cu_of(lens), device=DEV, dtype=torch.int32)
+  gd, hd, dyd = g.to(DEV), h.to(DEV), dy.to(DEV)
+  ones = torch.ones((), device=DEV).expand(C, sum(lens))
+  for grad in (dyd, ones):
+    torch.library.opcheck(torch.ops.associative_scan_triton.scan_causal_bwd,
+                          (grad, gd, hd, cu, 1, C, 64))
+  torch.library.opcheck(torch.ops.associative_scan_triton.scan_bidi_bwd,
+                        (dyd, dyd, hd, hd, gd, gd, cu, 1, C, 64))
+
+
+def test_torch_compile_dynamic_num_seq():
+  """With the grid from get_static_grid the compiled graph does not depend on
+  the number of packed sequences: after one dynamic-shape compile, other
+  counts of sequences (and total lengths) run without recompiling
+  (the reference's reason for get_static_grid, _grid.py:57-70)."""
+  import torch._dynamo
+  C = 6
+  static = ast.get_static_grid(512, 128, C)
+
+  def f(g, x, cu):
+    args = {"cu_seqlens": cu, "chunk_size": 128, "grid": (cu.shape[0] - 1,) + static}
+    return ast.scan_causal_compiled(g, x, args).square().sum()
+
+  torch._dynamo.reset()
+  cf = torch.compile(f, backend="aot_eager", fullgraph=True, dynamic=True)
+  for i, lens in enumerate(([100, 28, 7], [5, 300, 17, 1, 64], [512] * 4 + [3] * 5)):
+    g, x = make(lens, C, seed=40 + i)
+    cu = torch.tensor(cu_of(lens), device=DEV, dtype=torch.int32)
+    gd = g.to(DEV).requires_grad_(True)
+    xd = x.to(DEV).requires_grad_(True)
+    if i == 0:
+      loss = cf(gd, xd, cu)
+    else:
+      with torch._dynamo.config.patch(error_on_recompile=True):
+        loss = cf(gd, xd, cu)
+    loss.backward()
+    g2 = g.to(DEV).requires_grad_(True)
+    x2 = x.to(DEV).requires_grad_(True)
+    loss2 = f(g2, x2, cu)
+    loss2.backward()
+    torch.testing.assert_close(loss, loss2)
+    torch.testing.assert_close(gd.grad, g2.grad)
+    torch.testing.assert_close(xd.grad, x2.grad)
+
+
 def test_torch_compile_fullgraph():
   lens = [100, 28]
   C = 4
