@@ -1,13 +1,22 @@
 // libassocscan: gfx950 kernels and C ABI for the first-order linear
 // recurrence h[t] = g[t]*h[t-1] + x[t] over packed segments.
 //
-// Design (one wavefront per (segment, channel) pair, no LDS, no barriers):
+// Three walks share one sub-tile scan; the host picks one per call:
+//   * one wave per (segment, channel) item, carry in a register (short
+//     segments, every fp16/bf16 problem, the gate-product output);
+//   * one 8- or 16-wave workgroup per item, wave aggregates folded through
+//     LDS once per iteration (fp32 with long segments);
+//   * decoupled look-back over 1024-element tiles of the flat array, carries
+//     chained through a caller-provided workspace (fewer than 64 items,
+//     e.g. one long sequence).
+// Design of the sub-tile scan:
 //   * A segment of one row is walked in "sub-tiles" of 64 x 16 bytes: lane l
 //     owns one 16-byte vector (4 fp32 or 8 fp16/bf16 elements), so every
 //     global load/store instruction of the wave covers 1 KiB contiguously
 //     (global_load_dwordx4).  Vectors are aligned in memory; a segment start
 //     or end that falls inside a vector is handled by per-element masking on
-//     the first and last sub-tile only.
+//     the first and last sub-tile only (the look-back walk, whose tiles
+//     may hold several segments, masks every element of a tile that does).
 //   * Inside a sub-tile: each lane scans its own elements serially, the 64
 //     lane aggregates are combined by an inclusive DPP scan (row_shr 1/2/4/8,
 //     row_bcast 15/31), the exclusive prefix is taken with wave_shr:1, and the
@@ -1242,7 +1251,7 @@ __global__ void __launch_bounds__(4 * kWave) k_shift_pad(ShiftParams p) {
 // Slot words are (status << 32 | float bits), written and read with
 // agent-scope atomics (the 8 XCDs have separate L2 caches, so every poll is
 // a round trip past them); the workspace is zero-filled by a small kernel
-// before every launch.  Every wait is bounded: after lb_spin_limit
+// before every launch.  Every wait is bounded: after g_spin_limit (2^14 by default)
 // unsuccessful polls the waiting wave computes the missing predecessor's
 // aggregate from that tile's inputs itself, so progress never depends on
 // the order in which workgroups are scheduled.
