@@ -48,6 +48,10 @@ CONFIGS = {
   "cfg3": ("varlen causal fwd+bwd, 64 seqs U[16,8192], C=1024, bf16 storage, "
            "fp32 accumulate, g~U(0.5,1)", 64, 1024, None, "bfloat16", "causal",
            (0.5, 1.0)),
+  # not a BASELINE config: the segment-aware shift of _shift_pad.py at cfg5's
+  # tensor size (compiled semantics, pad at segment starts)
+  "shift": ("shift_pad backward=True (compiled form), B=8 C=1536 T=65536, "
+            "fp32", 8, 1536, 65536, "float32", "shift", None),
 }
 
 
@@ -115,7 +119,7 @@ def main():
   g = [gates() for _ in range(nbr)]
   x = [normal() for _ in range(nbr)]
   h = [torch.empty_like(x[0]) for _ in range(nbr)]
-  with_bwd = kind != "fwd"
+  with_bwd = kind not in ("fwd", "shift")
   if with_bwd:
     dy = [torch.rand(C, Tt, device=dev, generator=gen).to(dtype) for _ in range(nbr)]
     dx = [torch.empty_like(x[0]) for _ in range(nbr)]
@@ -125,7 +129,9 @@ def main():
       f"{torch.cuda.get_device_name(0)}")
 
   def fwd():
-    if kind == "bidi":
+    if kind == "shift":
+      _ops.shift_pad(x[0], h[0], cu, 0.0, backward=True, wrap=False)
+    elif kind == "bidi":
       _ops.scan_bidi_fwd(g[0], x[0], g[1], x[1], h[0], h[1], cu)
     else:
       _ops.scan_fwd(g[0], x[0], h[0], cu, reverse=False)
@@ -170,7 +176,7 @@ def main():
   log(f"[bench] timed {a.steps} steps in {wall:.3f} s wall; "
       f"fwd {np.mean(fwd_ms):.4f} ms, bwd {np.mean(bwd_ms):.4f} ms")
 
-  fwd_bytes = 3 * esize * N * nbr
+  fwd_bytes = (2 if kind == "shift" else 3) * esize * N * nbr
   bwd_bytes = 5 * esize * N * nbr if with_bwd else 0
   step_bytes = fwd_bytes + bwd_bytes
   gbs = step_bytes / (step_ms * 1e-3) / 1e9
@@ -178,7 +184,8 @@ def main():
   if with_bwd:
     dom, dom_ms, dom_bytes = "bwd", b_ms, bwd_bytes
   else:
-    dom, dom_ms, dom_bytes = "fwd", f_ms, fwd_bytes
+    dom = "shift_pad" if kind == "shift" else "fwd"
+    dom_ms, dom_bytes = f_ms, fwd_bytes
   achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
 
   # ---- parity of sampled rows (outside the timed region) ----
@@ -199,6 +206,11 @@ def main():
       return float(np.max(np.abs(got - ref) / (tol * s + tol * np.abs(ref))))
 
     for b in range(nbr):
+      if kind == "shift":  # a copy: bit-exact against the oracle
+        xs = x[0][rows].double().cpu().numpy()
+        ref = oracle.shift_pad(xs, cu_np, 0.0, backward=True, wrap=False)
+        ratios["out"] = 0.0 if np.array_equal(h[0][rows].double().cpu().numpy(), ref) else float("inf")
+        break
       rev = b == 1
       gs = g[b][rows].double().cpu().numpy()
       xs = x[b][rows].double().cpu().numpy()
