@@ -6,9 +6,9 @@
 //     segments, every fp16/bf16 problem, the gate-product output);
 //   * one 8- or 16-wave workgroup per item, wave aggregates folded through
 //     LDS once per iteration (fp32 with long segments);
-//   * decoupled look-back over 1024-element tiles of the flat array, carries
-//     chained through a caller-provided workspace (fewer than 64 items,
-//     e.g. one long sequence).
+//   * decoupled look-back over 4096-element tiles of the flat array (one
+//     4-wave workgroup each), carries chained through a caller-provided
+//     workspace (few items, e.g. one long sequence).
 // Design of the sub-tile scan:
 //   * A segment of one row is walked in "sub-tiles" of 64 x 16 bytes: lane l
 //     owns one 16-byte vector (4 fp32 or 8 fp16/bf16 elements), so every
@@ -1234,41 +1234,46 @@ __global__ void __launch_bounds__(4 * kWave) k_shift_pad(ShiftParams p) {
 // The walks above give each (segment, channel) item to one wave or one
 // workgroup, so a problem with few items (one long sequence, a handful of
 // channels) leaves most of the 256 CUs idle.  This walk cuts the flat array
-// of all rows into tiles of 1024 elements instead, so its parallelism is
-// the element count.  Wave w of workgroup b owns tile kLbWaves*b + w in scan
-// order (address order, or reverse address order for a reverse-direction
-// scan).  A tile may hold the end of one segment and the start of others
-// (or the end of one row and the start of the next): segment heads reset
-// the scan inside the tile.  Each tile
-//   1. loads its data and scans it locally;
-//   2. publishes its aggregate map (A, X) in its workspace slot -- or, if a
-//      segment starts inside the tile, directly its inclusive value, which
-//      no longer depends on earlier tiles;
-//   3. unless its first element is a segment head, looks back over the
-//      slots of the preceding tiles, 64 at a time (one per lane), composing
-//      aggregates with the same DPP scan until it meets an inclusive value;
-//   4. publishes its own inclusive value and writes its outputs.
+// of all rows into tiles of 4096 elements instead, so its parallelism is
+// the element count.  Workgroup b (kLbWaves waves) owns tile b in scan order
+// (address order, or reverse address order for a reverse-direction scan);
+// wave w owns part w of it, 1024 elements.  A part may hold the end of one
+// segment and the start of others (or the end of one row and the start of
+// the next): segment heads reset the scan inside it.  Each tile
+//   1. loads its data and scans it locally, one part per wave, and the part
+//      maps meet in LDS;
+//   2. (wave 0) publishes the tile's aggregate map (A, X) in its workspace
+//      slot -- or, if a segment starts inside the tile, directly its
+//      inclusive value, which no longer depends on earlier tiles;
+//   3. (wave 0) unless its first element in a segment is a head, looks back
+//      over the slots of the preceding tiles, 64 at a time (one per lane),
+//      composing aggregates with the same DPP scan until it meets an
+//      inclusive value, and publishes its own inclusive value;
+//   4. every wave takes the tile carry through the parts before its own and
+//      writes its outputs.
 // Slot words are (status << 32 | float bits), written and read with
 // agent-scope atomics (the 8 XCDs have separate L2 caches, so every poll is
 // a round trip past them); the workspace is zero-filled by a small kernel
-// before every launch.  Every wait is bounded: after g_spin_limit (2^14 by default)
-// unsuccessful polls the waiting wave computes the missing predecessor's
-// aggregate from that tile's inputs itself, so progress never depends on
-// the order in which workgroups are scheduled.
+// before every launch.  Every wait is bounded: after g_spin_limit (2^14 by
+// default) unsuccessful polls the waiting wave computes the missing
+// predecessor's map from that tile's inputs itself, so progress never
+// depends on the order in which workgroups are scheduled.
 //
 // Measured on MI355X, a poll round trip under full HBM load costs about as
 // much as a tile's own loads, so with many items the per-item walks (which
 // need no inter-workgroup communication) stream faster; the host picks this
-// walk only for problems with few items (lb_use).
+// walk only for problems with few items (lb_use).  Which predecessor a tile
+// meets as inclusive depends on timing, so the last bits of the results can
+// vary from run to run.
 // ===========================================================================
-// Tiles are 1024 elements for every element type: 4 sub-tiles of 64 lanes x
+// Parts are 1024 elements for every element type: 4 sub-tiles of 64 lanes x
 // 4 fp32, or 2 sub-tiles of 64 lanes x 8 fp16/bf16.
 template <class IO>
-constexpr int LbU = IO::V == 4 ? 4 : 2;  // sub-tiles per tile
+constexpr int LbU = IO::V == 4 ? 4 : 2;  // sub-tiles per part
 template <class IO>
-constexpr int64_t LbTileVec = static_cast<int64_t>(LbU<IO>) * kWave;
-constexpr int64_t kLbTileElems = 1024;
-constexpr int kLbWaves = 4;  // tiles (waves) per workgroup
+constexpr int64_t LbTileVec = static_cast<int64_t>(LbU<IO>) * kWave;  // per part
+constexpr int kLbWaves = 4;  // parts (waves) per workgroup tile
+constexpr int64_t kLbTileElems = 1024 * kLbWaves;  // elements per tile
 
 typedef unsigned long long u64;
 // One carry slot per tile, two tagged words: x holds (status << 32 | value)
@@ -1644,6 +1649,7 @@ struct FwdTile {
   float A, X;
   int F;
   bool need_carry;
+  bool any;  // some element of the part lies in a segment
 };
 
 // Elements of vector vi inside the tensor (bit j = memory index j).
@@ -1723,17 +1729,21 @@ __device__ inline void fwd_tile_local(const FwdPtrs& p, const LbGeo& geo,
       lb_compose(s.A, s.X, s.F, s.sc[u].ta, s.sc[u].tx, s.sc[u].tf);
     }
     s.need_carry = ti.phead < 0;
+    s.any = true;
     return;
   }
+  uint32_t anyv = 0;
 #pragma unroll
   for (int u = 0; u < LbU<IO>; ++u) {
     const int64_t vi = lb_vec<IO, REV>(geo, t, u, lane);
     uint32_t in2, tail;
     lb_flags<IO, REV>(geo, ti, vi, in2, s.valid[u], s.head[u], tail);
+    anyv |= s.valid[u];
     s.sc[u] = fwd_local_seg<IO, REV>(s.g[u], s.x[u], s.valid[u], s.head[u]);
     lb_compose(s.A, s.X, s.F, s.sc[u].ta, s.sc[u].tx, s.sc[u].tf);
   }
   s.need_carry = lb_needs_carry<IO, REV>(s.valid, s.head);
+  s.any = __builtin_amdgcn_ballot_w64(anyv != 0) != 0;
 }
 
 // Composes the maps of the tiles before t (scan order) until an inclusive
@@ -1835,6 +1845,41 @@ __device__ __attribute__((noinline)) void fwd_tile_map(const FwdPtrs p, const Lb
   }
 }
 
+// A workgroup tile is kLbWaves consecutive parts, one per wave.  The waves
+// share their part maps through LDS; wave 0 composes them into the tile
+// map, publishes it, looks back and hands the tile's carry-in to the others.
+struct LbPart {
+  float a, x;
+  int f;      // a segment head lies inside the part
+  int flags;  // bit 1: some element lies in a segment; bit 0: needs a carry
+};
+
+// Tile map (A, X, F) from the parts and whether the tile needs a carry (the
+// first part that holds segment elements needs one).
+__device__ inline bool lb_tile_from_parts(const LbPart* parts, float& A,
+                                          float& X, int& F) {
+  A = 1.0f;
+  X = 0.0f;
+  F = 0;
+  int nc = -1;
+#pragma unroll
+  for (int k = 0; k < kLbWaves; ++k) {
+    const LbPart q = parts[k];
+    lb_compose(A, X, F, q.a, q.x, q.f);
+    if (nc < 0 && (q.flags & 2)) nc = q.flags & 1;
+  }
+  return nc > 0;
+}
+
+// Carry into part wv from the tile's carry-in.
+__device__ inline float lb_part_carry(const LbPart* parts, int wv, float carry) {
+  for (int k = 0; k < wv; ++k) {
+    const LbPart q = parts[k];
+    carry = q.f ? q.x : fmaf(q.a, carry, q.x);
+  }
+  return carry;
+}
+
 struct LbFwdParams {
   LbGeo geo;
   FwdPtrs br[2];
@@ -1843,37 +1888,62 @@ struct LbFwdParams {
 
 template <class IO, int DIRS, bool ALN>
 __global__ void __launch_bounds__(kLbWaves* kWave) k_scan_fwd_lb(LbFwdParams p) {
+  __shared__ LbPart parts[kLbWaves];
+  __shared__ float tile_carry;
   const int lane = threadIdx.x % kWave;
-  const int64_t gt = static_cast<int64_t>(blockIdx.x) * kLbWaves + wave_id();
+  const int wv = wave_id();
+  const int64_t gt = blockIdx.x;
   const int br = gt >= p.geo.ntiles ? 1 : 0;
   const int64_t t = gt - br * p.geo.ntiles;
-  if (br >= p.geo.nbranch) return;
+  if (br >= p.geo.nbranch) return;  // whole workgroup
   LbSlot* slots = p.slots + br * p.geo.ntiles;
   auto run = [&](auto rev_tag) {
     constexpr bool REV = decltype(rev_tag)::value;
     constexpr int V = IO::V;
-    const FwdPtrs& q = p.br[br];
+    const FwdPtrs q = p.br[br];
     FwdTile<IO> s;
-    fwd_tile_local<IO, REV, ALN>(q, p.geo, t, lane, s);
-    if (lane == 0) {
-      if (s.F) {
-        lb_put(&slots[t].x, kLbIncl, s.X);
-      } else {
-        lb_put(&slots[t].a, kLbAgg, s.A);
-        lb_put(&slots[t].x, kLbAgg, s.X);
+    fwd_tile_local<IO, REV, ALN>(q, p.geo, t * kLbWaves + wv, lane, s);
+    if (lane == 0)
+      parts[wv] = LbPart{s.A, s.X, s.F, (s.any ? 2 : 0) | (s.need_carry ? 1 : 0)};
+    __syncthreads();
+    if (wv == 0) {
+      float A, X;
+      int F;
+      const bool need = lb_tile_from_parts(parts, A, X, F);
+      if (lane == 0) {
+        if (F) {
+          lb_put(&slots[t].x, kLbIncl, X);
+        } else {
+          lb_put(&slots[t].a, kLbAgg, A);
+          lb_put(&slots[t].x, kLbAgg, X);
+        }
+      }
+      float carry = 0.0f;
+      if (need)
+        carry = lb_lookback(p.geo, slots, t, lane,
+                            [&](int64_t j, float& a, float& x, int& f) {
+                              a = 1.0f;
+                              x = 0.0f;
+                              f = 0;
+                              for (int k = 0; k < kLbWaves; ++k) {
+                                float ma, mx;
+                                int mf;
+                                fwd_tile_map<IO, REV, ALN>(q, p.geo, j * kLbWaves + k,
+                                                           lane, ma, mx, mf);
+                                lb_compose(a, x, f, ma, mx, mf);
+                              }
+                            });
+      if (lane == 0) {
+        if (!F) lb_put(&slots[t].x, kLbIncl, fmaf(A, carry, X));
+        tile_carry = carry;
       }
     }
-    float carry = 0.0f;
-    if (s.need_carry)
-      carry = lb_lookback(p.geo, slots, t, lane,
-                          [&](int64_t j, float& a, float& x, int& f) {
-                            fwd_tile_map<IO, REV, ALN>(q, p.geo, j, lane, a, x, f);
-                          });
-    if (!s.F && lane == 0)
-      lb_put(&slots[t].x, kLbIncl, fmaf(s.A, carry, s.X));
+    __syncthreads();
+    float carry = lb_part_carry(parts, wv, tile_carry);
+    const int64_t pt = t * kLbWaves + wv;
 #pragma unroll
     for (int u = 0; u < LbU<IO>; ++u) {
-      const int64_t vi = lb_vec<IO, REV>(p.geo, t, u, lane);
+      const int64_t vi = lb_vec<IO, REV>(p.geo, pt, u, lane);
       float hf[V];
       fwd_apply_seg<IO, REV>(s.g[u], s.x[u], s.valid[u], s.head[u], s.sc[u],
                              carry, hf);
@@ -1894,10 +1964,11 @@ struct BwdTile {
   uint32_t valid[LbU<IO>], head[LbU<IO>], tail[LbU<IO>];
   float gprev[LbU<IO>];
   SegScan sc[LbU<IO>];
-  float hn;  // state just after the tile in B order (0 outside the tensor)
+  float hn;  // state just after the part in B order (0 outside the tensor)
   float A, X;
   int F;
   bool need_carry;
+  bool any;  // some element of the part lies in a segment
 };
 
 template <class IO, bool REV, bool ALN>
@@ -1956,19 +2027,23 @@ __device__ inline void bwd_tile_local(const BwdPtrs& p, const LbGeo& geo,
       lb_compose(s.A, s.X, s.F, s.sc[u].ta, s.sc[u].tx, s.sc[u].tf);
     }
     s.need_carry = ti.phead < 0;
+    s.any = true;
     return;
   }
+  uint32_t anyv = 0;
 #pragma unroll
   for (int u = 0; u < LbU<IO>; ++u) {
     const int64_t vi = lb_vec<IO, REV>(geo, t, u, lane);
     uint32_t in2;
     lb_flags<IO, REV>(geo, ti, vi, in2, s.valid[u], s.head[u], s.tail[u]);
+    anyv |= s.valid[u];
     s.sc[u] = bwd_local_seg<IO, REV>(s.g[u], s.y[u], s.valid[u], s.head[u], cg,
                                      s.gprev[u]);
     cg = readlane(s.g[u][jl], kWave - 1);
     lb_compose(s.A, s.X, s.F, s.sc[u].ta, s.sc[u].tx, s.sc[u].tf);
   }
   s.need_carry = lb_needs_carry<IO, REV>(s.valid, s.head);
+  s.any = __builtin_amdgcn_ballot_w64(anyv != 0) != 0;
 }
 
 template <class IO, bool REV, bool ALN>
@@ -2021,38 +2096,63 @@ struct LbBwdParams {
 // 3 = branch 0 causal / branch 1 anti-causal.
 template <class IO, int DIRS, bool ALN>
 __global__ void __launch_bounds__(kLbWaves* kWave) k_scan_bwd_lb(LbBwdParams p) {
+  __shared__ LbPart parts[kLbWaves];
+  __shared__ float tile_carry;
   const int lane = threadIdx.x % kWave;
-  const int64_t gt = static_cast<int64_t>(blockIdx.x) * kLbWaves + wave_id();
+  const int wv = wave_id();
+  const int64_t gt = blockIdx.x;
   const int br = gt >= p.geo.ntiles ? 1 : 0;
   const int64_t t = gt - br * p.geo.ntiles;
-  if (br >= p.geo.nbranch) return;
+  if (br >= p.geo.nbranch) return;  // whole workgroup
   LbSlot* slots = p.slots + br * p.geo.ntiles;
   auto run = [&](auto rev_tag) {
     constexpr bool REV = decltype(rev_tag)::value;
     constexpr int V = IO::V;
     constexpr int jf = mem_idx<V, REV>(0);
-    const BwdPtrs& q = p.br[br];
+    const BwdPtrs q = p.br[br];
+    const int64_t pt = t * kLbWaves + wv;
     BwdTile<IO> s;
-    bwd_tile_local<IO, REV, ALN>(q, p.geo, t, lane, s);
-    if (lane == 0) {
-      if (s.F) {
-        lb_put(&slots[t].x, kLbIncl, s.X);
-      } else {
-        lb_put(&slots[t].a, kLbAgg, s.A);
-        lb_put(&slots[t].x, kLbAgg, s.X);
+    bwd_tile_local<IO, REV, ALN>(q, p.geo, pt, lane, s);
+    if (lane == 0)
+      parts[wv] = LbPart{s.A, s.X, s.F, (s.any ? 2 : 0) | (s.need_carry ? 1 : 0)};
+    __syncthreads();
+    if (wv == 0) {
+      float A, X;
+      int F;
+      const bool need = lb_tile_from_parts(parts, A, X, F);
+      if (lane == 0) {
+        if (F) {
+          lb_put(&slots[t].x, kLbIncl, X);
+        } else {
+          lb_put(&slots[t].a, kLbAgg, A);
+          lb_put(&slots[t].x, kLbAgg, X);
+        }
+      }
+      float carry = 0.0f;
+      if (need)
+        carry = lb_lookback(p.geo, slots, t, lane,
+                            [&](int64_t j, float& a, float& x, int& f) {
+                              a = 1.0f;
+                              x = 0.0f;
+                              f = 0;
+                              for (int k = 0; k < kLbWaves; ++k) {
+                                float ma, mx;
+                                int mf;
+                                bwd_tile_map<IO, REV, ALN>(q, p.geo, j * kLbWaves + k,
+                                                           lane, ma, mx, mf);
+                                lb_compose(a, x, f, ma, mx, mf);
+                              }
+                            });
+      if (lane == 0) {
+        if (!F) lb_put(&slots[t].x, kLbIncl, fmaf(A, carry, X));
+        tile_carry = carry;
       }
     }
-    float carry = 0.0f;
-    if (s.need_carry)
-      carry = lb_lookback(p.geo, slots, t, lane,
-                          [&](int64_t j, float& a, float& x, int& f) {
-                            bwd_tile_map<IO, REV, ALN>(q, p.geo, j, lane, a, x, f);
-                          });
-    if (!s.F && lane == 0)
-      lb_put(&slots[t].x, kLbIncl, fmaf(s.A, carry, s.X));
+    __syncthreads();
+    float carry = lb_part_carry(parts, wv, tile_carry);
 #pragma unroll
     for (int u = 0; u < LbU<IO>; ++u) {
-      const int64_t vi = lb_vec<IO, REV>(p.geo, t, u, lane);
+      const int64_t vi = lb_vec<IO, REV>(p.geo, pt, u, lane);
       const float hin = (u + 1 < LbU<IO>) ? readlane(s.h[u + 1][jf], 0) : s.hn;
       float dx[V], dg[V];
       bwd_apply_seg<IO, REV>(s.g[u], s.y[u], s.h[u], s.valid[u], s.head[u],
@@ -2137,12 +2237,11 @@ int launch(const void* fn, int64_t blocks, int waves_per_block, Params& p,
 // predecessor itself (a test hook can lower it to exercise that path).
 uint32_t g_spin_limit = 1u << 14;
 
-// One wave per tile and no grid-stride loop: every tile needs its own wave.
-bool lb_grid_fits(int64_t tiles) {
-  return (tiles + kLbWaves - 1) / kLbWaves <= kMaxGrid;
-}
+// One workgroup per tile and no grid-stride loop: every tile needs its own
+// workgroup.
+bool lb_grid_fits(int64_t tiles) { return tiles <= kMaxGrid; }
 
-// Tiles of the look-back walk: 1024 elements each, from the start of the
+// Tiles of the look-back walk: 4096 elements each, from the start of the
 // phase frame (the vectors of every element type divide 1024).
 int64_t lb_ntiles(int64_t n, int phase) {
   return (phase + n + kLbTileElems - 1) / kLbTileElems;
@@ -2153,18 +2252,25 @@ int64_t lb_bytes(int64_t n, int v, int nbranch) {
   return lb_ntiles(n, v - 1) * nbranch * static_cast<int64_t>(sizeof(LbSlot));
 }
 
-// Walk choice: the look-back walk for problems with fewer (segment, channel)
-// items than kLbMaxItems (each item of the other walks is one wave or one
-// workgroup, which leaves most CUs idle), the per-item walks otherwise.  The
-// crossover was measured on MI355X (fp32 and bf16, 2^27 elements): at 16
-// items the look-back walk is 3.5x faster, at 64 the two are even, and at
-// 128 the per-item walks are 1.7x faster.  The look-back kernels also keep
-// row offsets and segment indices in 32 bits, and need one wave per tile.
-constexpr int64_t kLbMaxItems = 64;
-bool lb_use(int64_t S, int64_t C, int64_t T, int nbranch) {
+// Walk choice: the look-back walk for problems with few (segment, channel)
+// items (each item of the other walks is one wave or one workgroup, which
+// leaves most CUs idle), the per-item walks otherwise.  The crossover was
+// measured on MI355X (2^27 elements): fp32 -- look-back 1.4x faster at 64
+// items, 1.25x slower at 128; fp16/bf16 (one wave per item, no workgroup
+// walk) -- look-back 1.9x faster at 128 items, even at 256, 2x slower at
+// 512.  The look-back kernels also keep row offsets and segment indices in
+// 32 bits, and need one workgroup per tile.
+#ifndef ASC_LB_MAX_ITEMS_F32
+#define ASC_LB_MAX_ITEMS_F32 96
+#endif
+#ifndef ASC_LB_MAX_ITEMS_HALF
+#define ASC_LB_MAX_ITEMS_HALF 192
+#endif
+bool lb_use(int64_t S, int64_t C, int64_t T, int nbranch, int v) {
   if (S <= 0 || C <= 0 || T <= 0) return false;
   if (T >= (int64_t(1) << 30) || S >= (int64_t(1) << 30)) return false;
-  if (S * C * nbranch >= kLbMaxItems) return false;
+  const int64_t max_items = v == 4 ? ASC_LB_MAX_ITEMS_F32 : ASC_LB_MAX_ITEMS_HALF;
+  if (S * C * nbranch > max_items) return false;
   return lb_grid_fits(lb_ntiles(C * T, kLbTileElems - 1) * nbranch);
 }
 
@@ -2325,7 +2431,7 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
   const bool wa = a != nullptr;
   const int64_t items = p.geo.items * nbranch;
   if (!wa && ws && reinterpret_cast<uintptr_t>(ws) % 32 == 0 &&
-      lb_use(S, C, T, nbranch)) {
+      lb_use(S, C, T, nbranch, v)) {
     LbFwdParams q{};
     q.geo = LbGeo{cu, cu_dtype == ASC_CU_I64, S, C, T, C * T, p.geo.phase,
                   0, 0, nbranch, g_spin_limit};
@@ -2342,8 +2448,7 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
         case ASC_F16: fn = pick_fwd_lb<IoF16>(dirs, aln); break;
         default: fn = pick_fwd_lb<IoBF16>(dirs, aln); break;
       }
-      const int64_t tiles = q.geo.ntiles * nbranch;
-      return launch(fn, (tiles + kLbWaves - 1) / kLbWaves, kLbWaves, q, stream);
+      return launch(fn, q.geo.ntiles * nbranch, kLbWaves, q, stream);
     }
   }
   const int nw = wa ? 0 : pick_walk(S, T, v, false);
@@ -2408,7 +2513,7 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
   p.dy_rs = dy_rs;
   const int64_t items = p.geo.items * nbranch;
   if (!dyc && ws && reinterpret_cast<uintptr_t>(ws) % 32 == 0 &&
-      lb_use(S, C, T, nbranch)) {
+      lb_use(S, C, T, nbranch, v)) {
     LbBwdParams q{};
     q.geo = LbGeo{cu, cu_dtype == ASC_CU_I64, S, C, T, C * T, p.geo.phase,
                   0, 0, nbranch, g_spin_limit};
@@ -2425,8 +2530,7 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
         case ASC_F16: fn = pick_bwd_lb<IoF16>(dirs, aln); break;
         default: fn = pick_bwd_lb<IoBF16>(dirs, aln); break;
       }
-      const int64_t tiles = q.geo.ntiles * nbranch;
-      return launch(fn, (tiles + kLbWaves - 1) / kLbWaves, kLbWaves, q, stream);
+      return launch(fn, q.geo.ntiles * nbranch, kLbWaves, q, stream);
     }
   }
   const int nw = pick_walk(S, T, v, true);
@@ -2460,7 +2564,7 @@ int64_t asc_scan_workspace_bytes(int64_t num_seq, int64_t num_channels,
     return ASC_E_ARG;
   if (num_channels > 0 && seq_stride > (INT64_MAX / 64) / num_channels)
     return ASC_E_SIZE;
-  if (!lb_use(num_seq, num_channels, seq_stride, nbranch)) return 0;
+  if (!lb_use(num_seq, num_channels, seq_stride, nbranch, 16 / es)) return 0;
   return lb_bytes(num_channels * seq_stride, 16 / es, nbranch);
 }
 

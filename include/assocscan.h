@@ -20,13 +20,14 @@
  * Workspace: the scan entry points take an optional caller-owned device
  * buffer (32-byte aligned, asc_scan_workspace_bytes() bytes).  Problems
  * with few (segment, channel) items -- one long sequence, a handful of
- * channels -- need it: with it they run a single-pass decoupled look-back
- * walk over tiles of 1024 elements that keeps every CU busy (the buffer
+ * channels -- want it: with it they run a single-pass decoupled look-back
+ * walk over tiles of 4096 elements that keeps every CU busy (the buffer
  * holds one 16-byte carry slot per tile and is cleared by the call itself,
  * on `stream`).  Every other problem, and any call given NULL or a buffer
  * too small, runs the workspace-free walks (one wave or one workgroup per
- * item).  Results agree to fp32 rounding.  Two calls that run at the same
- * time must not share a workspace.
+ * item).  Results agree to fp32 rounding; the workspace-free walks are
+ * bitwise reproducible, the look-back walk's last bits can vary from run
+ * to run.  Two calls that run at the same time must not share a workspace.
  *
  * The reference is the Triton package associative-scan-triton 1.0.0; the
  * citations below name the reference function each entry point replaces.

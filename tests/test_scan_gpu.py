@@ -685,13 +685,24 @@ def test_time_constant_gradient(dtype, lens, C, compiled):
     return y.detach(), gd.grad, xd.grad
 
   T = sum(lens)
+  from associative_scan_triton import _lib
+  # few items run the look-back walk for both gradients (its last bits may
+  # vary from run to run); otherwise the time-constant path must reproduce
+  # the materialised gradient bit for bit
+  lookback = _lib.load().asc_scan_workspace_bytes(
+    len(lens), C, T, _lib.dtype_code(g), 1) > 0
   for loss_of, dense in (
       (lambda y: y.sum().backward(), torch.ones(C, T, dtype=dtype, device=DEV)),
       (lambda y: (y.sum(-1) * w).sum().backward(),
        w[:, None].expand(C, T).contiguous())):
     y1, dg1, dx1 = grads(loss_of)
     y2, dg2, dx2 = grads(lambda y: y.backward(dense))
-    assert torch.equal(dx1, dx2) and torch.equal(dg1, dg2)
+    if lookback:
+      tol = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
+      torch.testing.assert_close(dx1, dx2, **tol)
+      torch.testing.assert_close(dg1, dg2, **tol)
+    else:
+      assert torch.equal(dx1, dx2) and torch.equal(dg1, dg2)
     dx_ref, dg_ref = oracle_bwd(dense.cpu(), g, npf(y1), lens)
     check_close(dx1, dx_ref, dtype, "dx")
     check_close(dg1, dg_ref, dtype, "dg")
