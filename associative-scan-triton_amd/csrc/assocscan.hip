@@ -6,8 +6,8 @@
 //     segments, every fp16/bf16 problem, the gate-product output);
 //   * one 8- or 16-wave workgroup per item, wave aggregates folded through
 //     LDS once per iteration (fp32 with long segments);
-//   * decoupled look-back over 4096-element tiles of the flat array (one
-//     4-wave workgroup each), carries chained through a caller-provided
+//   * decoupled look-back over 16384-element tiles of the flat array (one
+//     16-wave workgroup each), carries chained through a caller-provided
 //     workspace (few items, e.g. one long sequence).
 // Design of the sub-tile scan:
 //   * A segment of one row is walked in "sub-tiles" of 64 x 16 bytes: lane l
@@ -1234,7 +1234,7 @@ __global__ void __launch_bounds__(4 * kWave) k_shift_pad(ShiftParams p) {
 // The walks above give each (segment, channel) item to one wave or one
 // workgroup, so a problem with few items (one long sequence, a handful of
 // channels) leaves most of the 256 CUs idle.  This walk cuts the flat array
-// of all rows into tiles of 4096 elements instead, so its parallelism is
+// of all rows into tiles of 16384 elements instead, so its parallelism is
 // the element count.  Workgroup b (kLbWaves waves) owns tile b in scan order
 // (address order, or reverse address order for a reverse-direction scan);
 // wave w owns part w of it, 1024 elements.  A part may hold the end of one
@@ -1267,13 +1267,27 @@ __global__ void __launch_bounds__(4 * kWave) k_shift_pad(ShiftParams p) {
 // vary from run to run.
 // ===========================================================================
 // Parts are 1024 elements for every element type: 4 sub-tiles of 64 lanes x
-// 4 fp32, or 2 sub-tiles of 64 lanes x 8 fp16/bf16.
+// 4 fp32, or 2 sub-tiles of 64 lanes x 8 fp16/bf16 (ASC_LB_U_F32 sets the
+// fp32 part for experiments).
+#ifndef ASC_LB_U_F32
+#define ASC_LB_U_F32 4
+#endif
 template <class IO>
-constexpr int LbU = IO::V == 4 ? 4 : 2;  // sub-tiles per part
+constexpr int LbU = IO::V == 4 ? ASC_LB_U_F32 : 2;  // sub-tiles per part
 template <class IO>
 constexpr int64_t LbTileVec = static_cast<int64_t>(LbU<IO>) * kWave;  // per part
-constexpr int kLbWaves = 4;  // parts (waves) per workgroup tile
-constexpr int64_t kLbTileElems = 1024 * kLbWaves;  // elements per tile
+// 16 waves (16384-element tiles): a poll costs the same for any tile size,
+// so fewer, larger tiles stream faster (measured with one 2^27-element row:
+// 4.1 / 4.7 TB/s fwd / bwd fp32 against 3.3 / 4.0 with 4 waves; 8 waves
+// were no better than 4 at the occupancy their register use allows).
+#ifndef ASC_LB_WAVES
+#define ASC_LB_WAVES 16
+#endif
+constexpr int kLbWaves = ASC_LB_WAVES;  // parts (waves) per workgroup tile
+// Elements per part for v elements per vector (host side; matches LbU).
+constexpr int64_t lb_part_elems(int v) {
+  return v == 4 ? 256 * ASC_LB_U_F32 : 2 * 512;
+}
 
 typedef unsigned long long u64;
 // One carry slot per tile, two tagged words: x holds (status << 32 | value)
@@ -2241,37 +2255,39 @@ uint32_t g_spin_limit = 1u << 14;
 // workgroup.
 bool lb_grid_fits(int64_t tiles) { return tiles <= kMaxGrid; }
 
-// Tiles of the look-back walk: 4096 elements each, from the start of the
+// Tiles of the look-back walk: kLbWaves parts each, from the start of the
 // phase frame (the vectors of every element type divide 1024).
-int64_t lb_ntiles(int64_t n, int phase) {
-  return (phase + n + kLbTileElems - 1) / kLbTileElems;
+int64_t lb_ntiles(int64_t n, int phase, int v) {
+  const int64_t te = lb_part_elems(v) * kLbWaves;
+  return (phase + n + te - 1) / te;
 }
 
 // Workspace bytes for the worst-case phase (v - 1).
 int64_t lb_bytes(int64_t n, int v, int nbranch) {
-  return lb_ntiles(n, v - 1) * nbranch * static_cast<int64_t>(sizeof(LbSlot));
+  return lb_ntiles(n, v - 1, v) * nbranch * static_cast<int64_t>(sizeof(LbSlot));
 }
 
 // Walk choice: the look-back walk for problems with few (segment, channel)
 // items (each item of the other walks is one wave or one workgroup, which
-// leaves most CUs idle), the per-item walks otherwise.  The crossover was
-// measured on MI355X (2^27 elements): fp32 -- look-back 1.4x faster at 64
-// items, 1.25x slower at 128; fp16/bf16 (one wave per item, no workgroup
-// walk) -- look-back 1.9x faster at 128 items, even at 256, 2x slower at
-// 512.  The look-back kernels also keep row offsets and segment indices in
-// 32 bits, and need one workgroup per tile.
+// leaves most CUs idle), the per-item walks otherwise.  Measured on MI355X
+// (2^27 elements): the look-back walk streams about 4.1 / 4.7 TB/s (fwd /
+// bwd) fp32 and 2.4 / 3.0 bf16 at any item count; 16-wave workgroups per
+// item reach 2.4 / 2.6 (fp32) and 1.5 / 1.3 (bf16) at 64 items, 4.4 / 4.6
+// and 2.8 / 2.3 at 128, and overtake beyond.  The look-back kernels also
+// keep row offsets and segment indices in 32 bits, and need one workgroup
+// per tile.
 #ifndef ASC_LB_MAX_ITEMS_F32
-#define ASC_LB_MAX_ITEMS_F32 96
+#define ASC_LB_MAX_ITEMS_F32 128
 #endif
 #ifndef ASC_LB_MAX_ITEMS_HALF
-#define ASC_LB_MAX_ITEMS_HALF 192
+#define ASC_LB_MAX_ITEMS_HALF 128
 #endif
 bool lb_use(int64_t S, int64_t C, int64_t T, int nbranch, int v) {
   if (S <= 0 || C <= 0 || T <= 0) return false;
   if (T >= (int64_t(1) << 30) || S >= (int64_t(1) << 30)) return false;
   const int64_t max_items = v == 4 ? ASC_LB_MAX_ITEMS_F32 : ASC_LB_MAX_ITEMS_HALF;
   if (S * C * nbranch > max_items) return false;
-  return lb_grid_fits(lb_ntiles(C * T, kLbTileElems - 1) * nbranch);
+  return lb_grid_fits(lb_ntiles(C * T, v - 1, v) * nbranch);
 }
 
 int fill_zero(void* ws, int64_t bytes, void* stream) {
@@ -2303,14 +2319,23 @@ int fill_zero(void* ws, int64_t bytes, void* stream) {
 #ifndef ASC_WG8_MIN_ITERS
 #define ASC_WG8_MIN_ITERS 4
 #endif
-int pick_walk(int64_t S, int64_t T, int v, bool bwd) {
-  // fp16/bf16: the workgroup walks hold 8 elements per lane in each of
-  // their ping-pong buffers (128+ VGPRs, spills in the backward); one wave
-  // per item streams faster at every segment length measured (bf16, 64K
-  // segments: 5.3 vs 4.6 TB/s forward, 5.3 vs 3.8 backward).
-  if (v != 4) return 0;
+#ifndef ASC_HALF_WG_MAX_ITEMS
+#define ASC_HALF_WG_MAX_ITEMS 512
+#endif
+int pick_walk(int64_t S, int64_t C, int64_t T, int nbranch, int v, bool bwd) {
   const int64_t mean = T / (S > 0 ? S : 1);
   const int64_t tile1 = static_cast<int64_t>(kUW) * kWave * v;  // per wave
+  if (v != 4) {
+    // fp16/bf16: the workgroup walks hold 8 elements per lane in each of
+    // their ping-pong buffers (128+ VGPRs, spills in the backward), so one
+    // wave per item streams faster once there are enough items to fill the
+    // chip (bf16, 64K segments x 12288 items: 5.3 vs 4.6 TB/s forward, 5.3
+    // vs 3.8 backward).  With fewer than 512 long items it leaves SIMDs
+    // idle and 16 waves per item win (bf16, 256 items of 512K: 4.9 / 3.3
+    // against 2.7 / 2.2 TB/s; even at 512 items).
+    const int64_t items = S * C * nbranch;
+    return items < ASC_HALF_WG_MAX_ITEMS && mean >= 16 * 16 * tile1 ? 16 : 0;
+  }
   const int64_t it16 = bwd ? ASC_BWD_WG16_MIN_ITERS : ASC_FWD_WG16_MIN_ITERS;
   if (mean >= it16 * 16 * tile1) return 16;
   if (mean >= static_cast<int64_t>(ASC_WG8_MIN_ITERS) * 8 * tile1) return 8;
@@ -2436,7 +2461,7 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
     q.geo = LbGeo{cu, cu_dtype == ASC_CU_I64, S, C, T, C * T, p.geo.phase,
                   0, 0, nbranch, g_spin_limit};
     q.geo.nvec = (q.geo.phase + q.geo.n + v - 1) / v;
-    q.geo.ntiles = lb_ntiles(q.geo.n, q.geo.phase);
+    q.geo.ntiles = lb_ntiles(q.geo.n, q.geo.phase, v);
     const int64_t need = q.geo.ntiles * nbranch * static_cast<int64_t>(sizeof(LbSlot));
     if (ws_bytes >= need) {
       for (int b = 0; b < nbranch; ++b) q.br[b] = p.br[b];
@@ -2451,12 +2476,14 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
       return launch(fn, q.geo.ntiles * nbranch, kLbWaves, q, stream);
     }
   }
-  const int nw = wa ? 0 : pick_walk(S, T, v, false);
+  const int nw = wa ? 0 : pick_walk(S, C, T, nbranch, v, false);
   if (nw) {
     const void* fn = nullptr;
-    // pick_walk returns workgroup walks for fp32 only
-    if (dtype != ASC_F32) return ASC_E_ARG;
-    fn = pick_fwd_wg<IoF32>(nw, dirs, aln);
+    switch (dtype) {
+      case ASC_F32: fn = pick_fwd_wg<IoF32>(nw, dirs, aln); break;
+      case ASC_F16: fn = pick_fwd_wg<IoF16>(nw, dirs, aln); break;
+      default: fn = pick_fwd_wg<IoBF16>(nw, dirs, aln); break;
+    }
     return launch(fn, items, nw, p, stream);
   }
   const void* fn = nullptr;
@@ -2518,7 +2545,7 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
     q.geo = LbGeo{cu, cu_dtype == ASC_CU_I64, S, C, T, C * T, p.geo.phase,
                   0, 0, nbranch, g_spin_limit};
     q.geo.nvec = (q.geo.phase + q.geo.n + v - 1) / v;
-    q.geo.ntiles = lb_ntiles(q.geo.n, q.geo.phase);
+    q.geo.ntiles = lb_ntiles(q.geo.n, q.geo.phase, v);
     const int64_t need = q.geo.ntiles * nbranch * static_cast<int64_t>(sizeof(LbSlot));
     if (ws_bytes >= need) {
       for (int b = 0; b < nbranch; ++b) q.br[b] = p.br[b];
@@ -2533,12 +2560,14 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
       return launch(fn, q.geo.ntiles * nbranch, kLbWaves, q, stream);
     }
   }
-  const int nw = pick_walk(S, T, v, true);
+  const int nw = pick_walk(S, C, T, nbranch, v, true);
   if (nw) {
     const void* fn = nullptr;
-    // pick_walk returns workgroup walks for fp32 only
-    if (dtype != ASC_F32) return ASC_E_ARG;
-    fn = pick_bwd_wg<IoF32>(nw, dirs, aln, dyc);
+    switch (dtype) {
+      case ASC_F32: fn = pick_bwd_wg<IoF32>(nw, dirs, aln, dyc); break;
+      case ASC_F16: fn = pick_bwd_wg<IoF16>(nw, dirs, aln, dyc); break;
+      default: fn = pick_bwd_wg<IoBF16>(nw, dirs, aln, dyc); break;
+    }
     return launch(fn, items, nw, p, stream);
   }
   const void* fn = nullptr;

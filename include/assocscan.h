@@ -21,7 +21,7 @@
  * buffer (32-byte aligned, asc_scan_workspace_bytes() bytes).  Problems
  * with few (segment, channel) items -- one long sequence, a handful of
  * channels -- want it: with it they run a single-pass decoupled look-back
- * walk over tiles of 4096 elements that keeps every CU busy (the buffer
+ * walk over tiles of 16384 elements that keeps every CU busy (the buffer
  * holds one 16-byte carry slot per tile and is cleared by the call itself,
  * on `stream`).  Every other problem, and any call given NULL or a buffer
  * too small, runs the workspace-free walks (one wave or one workgroup per

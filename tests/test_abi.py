@@ -73,22 +73,22 @@ def test_host_validation_codes():
 
 def test_workspace_bytes():
   lib = _lib.load()
-  # few (segment, channel) items: one 16-byte slot per tile of 4096 elements
+  # few (segment, channel) items: one 16-byte slot per tile of 16384 elements
   # (counted for the worst-case phase), per branch
   n = 4 * 1_000_000
   b1 = lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 0, 1)
   b2 = lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 0, 2)
-  assert b1 == 16 * -(-(n + 3) // 4096) and b2 == 2 * b1
-  assert lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 2, 1) == 16 * -(-(n + 7) // 4096)
-  # many items: the workspace-free walks, no workspace (thresholds: 96
-  # (segment, channel, branch) items for fp32, 192 for fp16/bf16)
+  assert b1 == 16 * -(-(n + 3) // 16384) and b2 == 2 * b1
+  assert lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 2, 1) == 16 * -(-(n + 7) // 16384)
+  # many items: the workspace-free walks, no workspace (threshold: 128
+  # (segment, channel, branch) items)
   assert lib.asc_scan_workspace_bytes(8, 1536, 524288, 0, 1) == 0
-  assert lib.asc_scan_workspace_bytes(1, 96, 4096, 0, 1) > 0
-  assert lib.asc_scan_workspace_bytes(1, 97, 4096, 0, 1) == 0
-  assert lib.asc_scan_workspace_bytes(1, 48, 4096, 0, 2) > 0
-  assert lib.asc_scan_workspace_bytes(1, 49, 4096, 0, 2) == 0
-  assert lib.asc_scan_workspace_bytes(2, 96, 4096, 2, 1) > 0
-  assert lib.asc_scan_workspace_bytes(2, 97, 4096, 1, 1) == 0
+  assert lib.asc_scan_workspace_bytes(1, 128, 4096, 0, 1) > 0
+  assert lib.asc_scan_workspace_bytes(1, 129, 4096, 0, 1) == 0
+  assert lib.asc_scan_workspace_bytes(1, 64, 4096, 0, 2) > 0
+  assert lib.asc_scan_workspace_bytes(1, 65, 4096, 0, 2) == 0
+  assert lib.asc_scan_workspace_bytes(2, 64, 4096, 2, 1) > 0
+  assert lib.asc_scan_workspace_bytes(2, 65, 4096, 1, 1) == 0
   # empty problems need nothing; invalid arguments are errors
   assert lib.asc_scan_workspace_bytes(0, 4, 128, 0, 1) == 0
   assert lib.asc_scan_workspace_bytes(1, 4, 128, 9, 1) < 0

@@ -166,15 +166,16 @@ def test_long_memory_error_vs_sequential_fp32():
 # few (segment, channel) items: the look-back walk over 1024-element tiles
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16],
+                         ids=["f32", "f16", "bf16"])
 @pytest.mark.parametrize("shape", [(1, [3_000_001]), (3, [1_000_000, 17, 999_983]),
                                    (1, [4096] * 40 + [7, 1, 2])],
                          ids=["one-row", "three-rows", "forty-segments"])
 def test_few_items_long_rows(dtype, shape):
-  """One or a few long rows (fewer than 64 items): every tile of 1024
-  elements is its own wave and carries chain through the workspace.  The
-  full result is checked against the oracle and against the
-  workspace-free walk on the same inputs."""
+  """One or a few long rows (few items): every tile of 4096 elements is its
+  own workgroup and carries chain through the workspace.  The full result
+  is checked against the oracle, and so is the workspace-free walk on the
+  same inputs."""
   C, lens = shape
   T = sum(lens)
   gen = _gen(11)
@@ -202,6 +203,11 @@ def test_few_items_long_rows(dtype, shape):
     cu_np = cu.cpu().numpy().astype(np.int64)
     ref_h = oracle.scan_fwd(npf(g), npf(x), cu_np, rev)
     check_close(h2, ref_h, dtype, "h (workspace-free walk)")
+    # (for these few long rows the workspace-free walk is a 16-wave
+    # workgroup per item, fp16/bf16 included)
+    dx_ref, dg_ref = oracle.scan_bwd(npf(dy), npf(g), npf(h), cu_np, causal=not rev)
+    check_close(dx2, dx_ref, dtype, "dx (workspace-free walk)")
+    check_close(dg2, dg_ref, dtype, "dg (workspace-free walk)")
     # the two walks agree to the output rounding
     tol = 1e-5 if dtype == torch.float32 else 1e-2
     s = max(1.0, float(h.float().square().mean().sqrt()))
