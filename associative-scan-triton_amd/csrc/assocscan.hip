@@ -3,9 +3,10 @@
 //
 // Three walks share one sub-tile scan; the host picks one per call:
 //   * one wave per (segment, channel) item, carry in a register (short
-//     segments, every fp16/bf16 problem, the gate-product output);
+//     segments, most fp16/bf16 problems, the gate-product output);
 //   * one 8- or 16-wave workgroup per item, wave aggregates folded through
-//     LDS once per iteration (fp32 with long segments);
+//     LDS once per iteration (long segments: fp32, and fp16/bf16 with few
+//     items);
 //   * decoupled look-back over 16384-element tiles of the flat array (one
 //     16-wave workgroup each), carries chained through a caller-provided
 //     workspace (few items, e.g. one long sequence).

@@ -172,7 +172,7 @@ def test_long_memory_error_vs_sequential_fp32():
                                    (1, [4096] * 40 + [7, 1, 2])],
                          ids=["one-row", "three-rows", "forty-segments"])
 def test_few_items_long_rows(dtype, shape):
-  """One or a few long rows (few items): every tile of 4096 elements is its
+  """One or a few long rows (few items): every tile of 16384 elements is its
   own workgroup and carries chain through the workspace.  The full result
   is checked against the oracle, and so is the workspace-free walk on the
   same inputs."""
