@@ -783,3 +783,60 @@ def test_graph_capture_replay(C, lens):
     torch.cuda.synchronize()
     if not lookback:
       assert all(torch.equal(a, b) for a, b in zip(got, (h, dx, dg)))
+
+
+# ---------------------------------------------------------------------------
+# shift_pad: the vectorised kernel (data and out of one phase) and the
+# element kernel (different phases), rows that straddle vectors, several
+# chunks per row, both edge rules
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("backward", [True, False])
+@pytest.mark.parametrize("wrap", [True, False])
+@pytest.mark.parametrize("offsets", [(0, 0), (1, 1), (3, 3), (1, 0)],
+                         ids=["aligned", "phase1", "phase3", "mixed"])
+def test_shift_pad_layouts(dtype, backward, wrap, offsets):
+  from associative_scan_triton import _ops
+  lens = [1, 700, 3, 5001, 2, 1300]          # rows of 7007: not a multiple of 4 or 8
+  C, L = 9, sum(lens)
+  gen = torch.Generator().manual_seed(17)
+  data = torch.randn(C, L, generator=gen).to(dtype)
+  cu_np = cu_of(lens)
+  cu = torch.tensor(cu_np, device=DEV, dtype=torch.int32)
+  od, oo = offsets
+  dbuf = torch.zeros(C * L + 8, dtype=dtype, device=DEV)
+  obuf = torch.full((C * L + 8,), 7.0, dtype=dtype, device=DEV)
+  dv = dbuf[od:od + C * L].view(C, L)
+  ov = obuf[oo:oo + C * L].view(C, L)
+  dv.copy_(data.to(DEV))
+  _ops.shift_pad(dv, ov, cu, -2.5, backward=backward, wrap=wrap)
+  ref = oracle.shift_pad(npf(data), cu_np, -2.5, backward, wrap=wrap)
+  assert torch.equal(ov.cpu(), torch.from_numpy(ref).to(dtype))
+  # nothing outside the output view is written
+  assert torch.all(obuf[:oo] == 7.0) and torch.all(obuf[oo + C * L:] == 7.0)
+
+
+def test_shift_pad_negative_boundary_and_raw_bits():
+  """A zero-length first segment puts the forward pad at position -1, which
+  counts from the row end (torch indexing in the reference); values move
+  as raw bits, NaN payloads included."""
+  from associative_scan_triton import _ops
+  C, L = 3, 2051
+  raw = torch.randint(-2**31, 2**31 - 1, (C, L), generator=torch.Generator().manual_seed(2),
+                      dtype=torch.int32)
+  raw[0, 5] = 0x7f800001          # a signalling NaN
+  raw[1, 9] = -0x00400001         # a negative NaN with a payload (0xffbfffff)
+  data = raw.view(torch.float32)
+  cu_np = np.array([0, 0, 700, L])
+  cu = torch.tensor(cu_np, device=DEV)
+  for backward in (True, False):
+    out = torch.empty(C, L, device=DEV)
+    _ops.shift_pad(data.to(DEV), out, cu, 0.0, backward=backward, wrap=False)
+    idx = torch.arange(L)
+    src = (idx - 1).clamp(min=0) if backward else (idx + 1).clamp(max=L - 1)
+    exp = raw[:, src].clone()
+    pads = cu_np[:-1] if backward else cu_np[1:] - 1
+    for q in pads:
+      exp[:, int(q) % L] = 0      # pad 0.0 has all-zero bits
+    assert torch.equal(out.cpu().view(torch.int32), exp)
