@@ -1026,23 +1026,24 @@ __device__ inline int64_t cu_at(const Geometry& geo, int64_t i) {
 }
 
 // Decodes item w; returns false for an empty segment.
-// SEG_MAJOR (the one-wave walk): channels go in blocks of kItemChanBlock;
-// inside a block, items w, w+1, ... are one segment of the block's
-// channels, then the next segment.  Waves that run at the same time then
-// work on segments of equal length (which keeps ragged varlen batches
-// streaming: cfg3 0.95 -> 0.76 ms against row-major order) while staying in
-// a few neighbouring rows (channel-major order over all C rows lost 8-14% on
-// uniform segments; 8-channel blocks cost at most 5% there).
-// Otherwise (the workgroup walks): the same segment of neighbouring
-// channels.
+// BLOCKS: channels go in blocks of kItemChanBlock; inside a block, items
+// w, w+1, ... are one segment of the block's channels, then the next
+// segment.  Waves (workgroups) that run at the same time then work on
+// segments of equal length in a few neighbouring rows.  One wave per item:
+// cfg3 (ragged varlen) 0.95 -> 0.76 ms against row-major order, uniform
+// segments within 5% (channel-major order over all C rows gained as much on
+// cfg3 but lost 8-14% on uniform segments).  Workgroup walks: +5-12% for
+// segments of 8K-32K fp32 elements, -2% from 64K, so the host sets
+// the order (the BLK instantiation) from the mean segment length.
+// Otherwise: the same segment of neighbouring channels (channel-major).
 constexpr int64_t kItemChanBlock = 8;
-template <bool SEG_MAJOR>
 __device__ inline bool item_range(const Geometry& geo, int64_t w, int& br,
-                                  int64_t& P0, int64_t& P1, int64_t& row) {
+                                  int64_t& P0, int64_t& P1, int64_t& row,
+                                  bool blocks) {
   br = w >= geo.items ? 1 : 0;
   const int64_t r = w - br * geo.items;
   int64_t s, c;
-  if (SEG_MAJOR) {
+  if (blocks) {
     // blocks of kItemChanBlock channels; inside a block the same segment of
     // its channels, then the next segment
     constexpr int64_t CB = kItemChanBlock;
@@ -1090,7 +1091,7 @@ __global__ void __launch_bounds__(kWPB* kWave) k_scan_fwd(FwdParams p) {
        w += stride) {
     int br;
     int64_t P0, P1, row;
-    if (!item_range<true>(p.geo, w, br, P0, P1, row)) continue;
+    if (!item_range(p.geo, w, br, P0, P1, row, true)) continue;
     const FwdPtrs& t = p.br[br];
     if (DIRS == 1 || (DIRS == 3 && br == 0))
       fwd_item<IO, false, ALN, WA>(t, P0, P1, lane);
@@ -1124,7 +1125,7 @@ __global__ void __launch_bounds__(kWPB* kWave) k_scan_bwd(BwdParams p) {
        w += stride) {
     int br;
     int64_t P0, P1, row;
-    if (!item_range<true>(p.geo, w, br, P0, P1, row)) continue;
+    if (!item_range(p.geo, w, br, P0, P1, row, true)) continue;
     const BwdPtrs& t = p.br[br];
     const float dyv = dyc_value<IO, DYC>(p, br, row);
     if (DIRS == 1 || (DIRS == 3 && br == 0))
@@ -1138,7 +1139,8 @@ __global__ void __launch_bounds__(kWPB* kWave) k_scan_bwd(BwdParams p) {
 #ifndef ASC_WG_ATTR
 #define ASC_WG_ATTR
 #endif
-template <class IO, int DIRS, bool ALN, int NW>
+// BLK: item order in channel blocks (item_range).
+template <class IO, int DIRS, bool ALN, int NW, bool BLK>
 __global__ void __launch_bounds__(NW* kWave) ASC_WG_ATTR k_scan_fwd_wg(FwdParams p) {
   __shared__ float2 agg[2 * NW];
   const int lane = threadIdx.x % kWave;
@@ -1147,7 +1149,7 @@ __global__ void __launch_bounds__(NW* kWave) ASC_WG_ATTR k_scan_fwd_wg(FwdParams
   for (int64_t item = blockIdx.x; item < W; item += gridDim.x) {
     int br;
     int64_t P0, P1, row;
-    if (!item_range<false>(p.geo, item, br, P0, P1, row)) continue;
+    if (!item_range(p.geo, item, br, P0, P1, row, BLK)) continue;
     const FwdPtrs& t = p.br[br];
     if (DIRS == 1 || (DIRS == 3 && br == 0))
       fwd_item_wg<IO, false, ALN, NW>(t, P0, P1, lane, wv, agg);
@@ -1157,7 +1159,7 @@ __global__ void __launch_bounds__(NW* kWave) ASC_WG_ATTR k_scan_fwd_wg(FwdParams
   }
 }
 
-template <class IO, int DIRS, bool ALN, int NW, bool DYC>
+template <class IO, int DIRS, bool ALN, int NW, bool DYC, bool BLK>
 __global__ void __launch_bounds__(NW* kWave) ASC_WG_ATTR k_scan_bwd_wg(BwdParams p) {
   __shared__ float2 agg[2 * NW];
   const int lane = threadIdx.x % kWave;
@@ -1166,7 +1168,7 @@ __global__ void __launch_bounds__(NW* kWave) ASC_WG_ATTR k_scan_bwd_wg(BwdParams
   for (int64_t item = blockIdx.x; item < W; item += gridDim.x) {
     int br;
     int64_t P0, P1, row;
-    if (!item_range<false>(p.geo, item, br, P0, P1, row)) continue;
+    if (!item_range(p.geo, item, br, P0, P1, row, BLK)) continue;
     const BwdPtrs& t = p.br[br];
     const float dyv = dyc_value<IO, DYC>(p, br, row);
     if (DIRS == 1 || (DIRS == 3 && br == 0))
@@ -2575,18 +2577,18 @@ int pick_walk(int64_t S, int64_t C, int64_t T, int nbranch, int v, bool bwd) {
   return 0;
 }
 
-template <class IO, int NW>
+template <class IO, int NW, bool BLK>
 const void* pick_fwd_wg(int dirs, bool aln) {
-#define ASC_F(D, A) reinterpret_cast<const void*>(&k_scan_fwd_wg<IO, D, A, NW>)
+#define ASC_F(D, A) reinterpret_cast<const void*>(&k_scan_fwd_wg<IO, D, A, NW, BLK>)
   if (dirs == 1) return aln ? ASC_F(1, true) : ASC_F(1, false);
   if (dirs == 2) return aln ? ASC_F(2, true) : ASC_F(2, false);
   return aln ? ASC_F(3, true) : ASC_F(3, false);
 #undef ASC_F
 }
 
-template <class IO, int NW>
+template <class IO, int NW, bool BLK>
 const void* pick_bwd_wg(int dirs, bool aln, bool dyc) {
-#define ASC_B(D, A, Y) reinterpret_cast<const void*>(&k_scan_bwd_wg<IO, D, A, NW, Y>)
+#define ASC_B(D, A, Y) reinterpret_cast<const void*>(&k_scan_bwd_wg<IO, D, A, NW, Y, BLK>)
   if (dyc) {  // single-branch calls only
     if (dirs == 1) return aln ? ASC_B(1, true, true) : ASC_B(1, false, true);
     return aln ? ASC_B(2, true, true) : ASC_B(2, false, true);
@@ -2598,14 +2600,19 @@ const void* pick_bwd_wg(int dirs, bool aln, bool dyc) {
 }
 
 template <class IO>
-const void* pick_fwd_wg(int nw, int dirs, bool aln) {
-  return nw == 16 ? pick_fwd_wg<IO, 16>(dirs, aln) : pick_fwd_wg<IO, 8>(dirs, aln);
+const void* pick_fwd_wg(int nw, int dirs, bool aln, bool blk) {
+  if (blk)
+    return nw == 16 ? pick_fwd_wg<IO, 16, true>(dirs, aln) : pick_fwd_wg<IO, 8, true>(dirs, aln);
+  return nw == 16 ? pick_fwd_wg<IO, 16, false>(dirs, aln) : pick_fwd_wg<IO, 8, false>(dirs, aln);
 }
 
 template <class IO>
-const void* pick_bwd_wg(int nw, int dirs, bool aln, bool dyc) {
-  return nw == 16 ? pick_bwd_wg<IO, 16>(dirs, aln, dyc)
-                  : pick_bwd_wg<IO, 8>(dirs, aln, dyc);
+const void* pick_bwd_wg(int nw, int dirs, bool aln, bool dyc, bool blk) {
+  if (blk)
+    return nw == 16 ? pick_bwd_wg<IO, 16, true>(dirs, aln, dyc)
+                    : pick_bwd_wg<IO, 8, true>(dirs, aln, dyc);
+  return nw == 16 ? pick_bwd_wg<IO, 16, false>(dirs, aln, dyc)
+                  : pick_bwd_wg<IO, 8, false>(dirs, aln, dyc);
 }
 
 template <class IO>
@@ -2652,6 +2659,12 @@ const void* pick_bwd(int dirs, bool aln, bool dyc) {
   if (dirs == 2) return aln ? ASC_B(2, true, false) : ASC_B(2, false, false);
   return aln ? ASC_B(3, true, false) : ASC_B(3, false, false);
 #undef ASC_B
+}
+
+// Item order of the workgroup walks: channel blocks up to a mean segment
+// of 32K elements, channel-major beyond (measured, fp32, see item_range).
+int wg_chan_blocks(int64_t S, int64_t T) {
+  return T / (S > 0 ? S : 1) <= 32768 ? 1 : 0;
 }
 
 int run_fwd(const void* const* g, const void* const* x, void* const* h,
@@ -2712,11 +2725,12 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
   }
   const int nw = wa ? 0 : pick_walk(S, C, T, nbranch, v, false);
   if (nw) {
+    const bool blk = wg_chan_blocks(S, T) != 0;
     const void* fn = nullptr;
     switch (dtype) {
-      case ASC_F32: fn = pick_fwd_wg<IoF32>(nw, dirs, aln); break;
-      case ASC_F16: fn = pick_fwd_wg<IoF16>(nw, dirs, aln); break;
-      default: fn = pick_fwd_wg<IoBF16>(nw, dirs, aln); break;
+      case ASC_F32: fn = pick_fwd_wg<IoF32>(nw, dirs, aln, blk); break;
+      case ASC_F16: fn = pick_fwd_wg<IoF16>(nw, dirs, aln, blk); break;
+      default: fn = pick_fwd_wg<IoBF16>(nw, dirs, aln, blk); break;
     }
     return launch(fn, items, nw, p, stream);
   }
@@ -2797,11 +2811,12 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
   }
   const int nw = pick_walk(S, C, T, nbranch, v, true);
   if (nw) {
+    const bool blk = wg_chan_blocks(S, T) != 0;
     const void* fn = nullptr;
     switch (dtype) {
-      case ASC_F32: fn = pick_bwd_wg<IoF32>(nw, dirs, aln, dyc); break;
-      case ASC_F16: fn = pick_bwd_wg<IoF16>(nw, dirs, aln, dyc); break;
-      default: fn = pick_bwd_wg<IoBF16>(nw, dirs, aln, dyc); break;
+      case ASC_F32: fn = pick_bwd_wg<IoF32>(nw, dirs, aln, dyc, blk); break;
+      case ASC_F16: fn = pick_bwd_wg<IoF16>(nw, dirs, aln, dyc, blk); break;
+      default: fn = pick_bwd_wg<IoBF16>(nw, dirs, aln, dyc, blk); break;
     }
     return launch(fn, items, nw, p, stream);
   }
