@@ -9,6 +9,8 @@ from __future__ import annotations
 import os
 import shutil
 import subprocess
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -21,11 +23,13 @@ LIB_PATH = PKG_DIR / LIB_NAME
 ARCH = os.environ.get("ASC_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
+# Symbols are hidden unless marked: only the extern "C" entry points (between
+# visibility pragmas in the sources) are exported.
 HIPCC_FLAGS = [
   "-O3",
   "-std=c++17",
   "-fPIC",
-  "-shared",
+  "-fvisibility=hidden",
   f"--offload-arch={ARCH}",
   "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
   "-Wall",
@@ -39,14 +43,7 @@ def hipcc() -> str:
   return path
 
 
-def build(verbose: bool = False, extra_flags: list[str] | None = None,
-          out: Path | None = None) -> Path:
-  """Compiles csrc/*.hip into one shared library and returns its path."""
-  out = Path(out) if out is not None else LIB_PATH
-  sources = sorted(str(p) for p in CSRC_DIR.glob("*.hip"))
-  tmp = out.with_name(out.name + f".tmp{os.getpid()}")
-  cmd = [hipcc(), *HIPCC_FLAGS, *(extra_flags or []), f"-I{INCLUDE_DIR}",
-         *sources, "-o", str(tmp)]
+def _run(cmd: list[str], verbose: bool) -> None:
   if verbose:
     print(" ".join(cmd), flush=True)
   res = subprocess.run(cmd, capture_output=True, text=True)
@@ -55,6 +52,30 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None,
       f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
   if verbose and (res.stdout or res.stderr):
     print(res.stdout, res.stderr, flush=True)
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None,
+          out: Path | None = None, jobs: int | None = None) -> Path:
+  """Compiles each csrc/*.hip to an object (in parallel), links them into one
+  shared library and returns its path."""
+  out = Path(out) if out is not None else LIB_PATH
+  sources = sorted(CSRC_DIR.glob("*.hip"))
+  if not sources:
+    raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
+  flags = [*HIPCC_FLAGS, *(extra_flags or []), f"-I{INCLUDE_DIR}",
+           f"-I{CSRC_DIR}"]
+  jobs = jobs or min(len(sources), int(os.environ.get("MAX_JOBS", "0"))
+                     or os.cpu_count() or 1)
+  with tempfile.TemporaryDirectory(prefix="asc_build_") as tmpdir:
+    objs = [Path(tmpdir) / (s.stem + ".o") for s in sources]
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
+      futs = [pool.submit(_run, [hipcc(), *flags, "-c", str(s), "-o", str(o)],
+                          verbose) for s, o in zip(sources, objs)]
+      for f in futs:
+        f.result()
+    tmp = out.with_name(out.name + f".tmp{os.getpid()}")
+    _run([hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}",
+          *[str(o) for o in objs], "-o", str(tmp)], verbose)
   os.replace(tmp, out)
   return out
 
