@@ -17,9 +17,10 @@
 //   * A segment of one row is walked in "sub-tiles" of 64 x 16 bytes: lane l
 //     owns one 16-byte vector (4 fp32 or 8 fp16/bf16 elements), so every
 //     global load/store instruction of the wave covers 1 KiB contiguously
-//     (global_load_dwordx4).  Vectors are aligned in memory; a segment start
-//     or end that falls inside a vector is handled by per-element masking on
-//     the first and last sub-tile only (the look-back walk, whose tiles
+//     (global_load_dwordx4).  Vectors are aligned in memory and sub-tiles
+//     start on 128-byte lines; a segment start or end that falls inside a
+//     sub-tile is handled by per-element masking on the first and last
+//     sub-tile only (the look-back walk, whose tiles
 //     may hold several segments, masks every element of a tile that does).
 //   * Inside a sub-tile: each lane scans its own elements serially, the 64
 //     lane aggregates are combined by an inclusive DPP scan (row_shr 1/2/4/8,
@@ -225,6 +226,8 @@ __device__ inline void wave_scan_mul(float& p) {
 // (origin = tensor base - phase*ES).  With ALN == false (tensors with
 // different phases) phase is 0 and every access is a scalar access.
 // ---------------------------------------------------------------------------
+constexpr int64_t kLineVecs = 8;  // 16-byte vectors per 128-byte line
+
 template <class IO, bool REV>
 struct Walk {
   int64_t P0, P1;  // element range [P0, P1), P1 > P0
@@ -239,6 +242,16 @@ struct Walk {
     constexpr int V = IO::V;
     v0 = P0 / V;
     v1 = (P1 - 1) / V;
+    // The first sub-tile in scan order is widened to start on a multiple
+    // of 8 vectors from the origin (a 128-byte line when the tensor base is
+    // 128-byte aligned, as torch's allocations are; the extra lanes lie
+    // outside the item and are masked like any edge element), so every
+    // later sub-tile covers exactly 8 lines.  Sub-tiles that start mid-line make each load and store touch
+    // one line more and split lines between consecutive sub-tiles
+    // (measured, cfg3-like ragged bf16 segments: +6% forward, +10%
+    // backward; aligned segments unchanged).
+    if (REV) v1 |= kLineVecs - 1;
+    else v0 &= ~(kLineVecs - 1);
     nv = v1 - v0 + 1;
     nsub = (nv + kWave - 1) / kWave;
     const bool tail_partial = REV ? (P0 % V) != 0 : (P1 % V) != 0;
