@@ -54,12 +54,6 @@
 #ifndef ASC_WAVES_PER_BLOCK
 #define ASC_WAVES_PER_BLOCK 1
 #endif
-#ifndef ASC_FWD_UNROLL
-#define ASC_FWD_UNROLL 4
-#endif
-#ifndef ASC_BWD_UNROLL
-#define ASC_BWD_UNROLL 2
-#endif
 // Sub-tiles per wave and iteration of the workgroup-cooperative kernels.
 #ifndef ASC_WG_UNROLL
 #define ASC_WG_UNROLL 1
