@@ -43,6 +43,7 @@ SIGNATURES = {
   "asc_scan_bwd_rowgrad": [_P, _L, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P],
   "asc_scan_bidi_fwd": [_P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _P, _L, _P],
   "asc_scan_bidi_bwd": [_P] * 11 + [_I, _L, _L, _L, _I, _P, _L, _P],
+  "asc_scan_bidi_bwd_rowgrad": [_P, _L, _P, _L] + [_P] * 9 + [_I, _L, _L, _L, _I, _P],
   "asc_shift_pad": [_P, _P, _P, _I, _L, _L, _L, _I, _D, _I, _I, _P],
 }
 RESTYPES = {

@@ -232,6 +232,65 @@ def scan_bidi_bwd(dyf: torch.Tensor, dyb: torch.Tensor, gf: torch.Tensor,
       _lib.ptr(ws), nb, _lib.stream_of(dev)))
 
 
+def scan_bidi_bwd_rowgrad(dyf: torch.Tensor, rsf: int, dyb: torch.Tensor,
+                          rsb: int, gf: torch.Tensor, gb: torch.Tensor,
+                          hf: torch.Tensor, hb: torch.Tensor,
+                          dxf: torch.Tensor, dgf: torch.Tensor,
+                          dxb: torch.Tensor, dgb: torch.Tensor,
+                          cu: torch.Tensor,
+                          num_channels: int | None = None) -> None:
+  """Backward of both branches for gradients constant along time (one value
+  per row, `rsf` / `rsb` elements apart, read from dyf / dyb.data_ptr())."""
+  lib = _lib.load()
+  dev = _lib.require_device(dyf, dyb, gf, gb, hf, hb, dxf, dgf, dxb, dgb, cu)
+  _check_same(hf, gf, gb, hb, dxf, dgf, dxb, dgb)
+  for d in (dyf, dyb):
+    if d.dtype != hf.dtype:
+      raise TypeError(f"dtype mismatch: {hf.dtype} vs {d.dtype}")
+  dt = _lib.dtype_code(hf)
+  cuc = _lib.cu_code(cu)
+  cu = cu.contiguous()
+  S, C, T = _geometry(hf, cu, num_channels)
+  with _OnDevice(dev):
+    _lib.check(lib.asc_scan_bidi_bwd_rowgrad(
+      dyf.data_ptr(), int(rsf), dyb.data_ptr(), int(rsb), gf.data_ptr(),
+      gb.data_ptr(), hf.data_ptr(), hb.data_ptr(), dxf.data_ptr(),
+      dgf.data_ptr(), dxb.data_ptr(), dgb.data_ptr(), cu.data_ptr(), cuc, S,
+      C, T, dt, _lib.stream_of(dev)))
+
+
+def scan_bidi_bwd_any(dyf: torch.Tensor | None, dyb: torch.Tensor | None,
+                      gf: torch.Tensor, gb: torch.Tensor, hf: torch.Tensor,
+                      hb: torch.Tensor, dxf: torch.Tensor, dgf: torch.Tensor,
+                      dxb: torch.Tensor, dgb: torch.Tensor, cu: torch.Tensor,
+                      num_channels: int | None = None) -> None:
+  """Bidirectional backward for any incoming gradient layouts.  None stands
+  for a branch whose output received no gradient (zero).  When both
+  gradients are constant along time (stride-0 expanded tensors, or None)
+  they are read one value per row, unless the geometry runs the look-back
+  walk; otherwise both are made contiguous, as the reference does
+  (scan_eager.py:161,166)."""
+  zero = None
+  if dyf is None or dyb is None:
+    zero = torch.zeros((), dtype=hf.dtype, device=hf.device)
+  rsf = 0 if dyf is None else row_constant_stride(dyf, hf, num_channels)
+  rsb = 0 if dyb is None else row_constant_stride(dyb, hb, num_channels)
+  if rsf is not None and rsb is not None:
+    lib = _lib.load()
+    cu_c = cu.contiguous()
+    S, C, T = _geometry(hf, cu_c, num_channels)
+    if not USE_WORKSPACE or lib.asc_scan_workspace_bytes(
+        S, C, T, _lib.dtype_code(hf), 2) <= 0:
+      scan_bidi_bwd_rowgrad(zero if dyf is None else dyf, rsf,
+                            zero if dyb is None else dyb, rsb, gf, gb, hf, hb,
+                            dxf, dgf, dxb, dgb, cu_c, num_channels)
+      return
+  dyf = torch.zeros_like(hf) if dyf is None else dyf.contiguous()
+  dyb = torch.zeros_like(hb) if dyb is None else dyb.contiguous()
+  scan_bidi_bwd(dyf, dyb, gf, gb, hf, hb, dxf, dgf, dxb, dgb, cu,
+                num_channels)
+
+
 def shift_pad(data: torch.Tensor, out: torch.Tensor, cu: torch.Tensor,
               pad_value: float, backward: bool, wrap: bool) -> None:
   """out <- segment-aware shift of a contiguous [C, L] tensor."""

@@ -70,7 +70,7 @@ def scan_causal_bwd_op(
 
 @scan_causal_bwd_op.register_fake
 def _(grad, gates, states, cu_seqlens, num_chunks, no_channels, chunk_size):
-  return torch.empty_like(gates), torch.empty_like(grad, memory_format=torch.contiguous_format)
+  return torch.empty_like(gates), torch.empty_like(states)
 
 
 def _scan_causal_setup_context(ctx, inputs, output) -> None:
@@ -142,30 +142,27 @@ def scan_bidi_bwd_op(
   no_channels: int,
   chunk_size: int,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-  """Backward of both branches in one launch.
+  """Backward of both branches in one launch.  Gradients that are constant
+  along time are read one value per row, not materialised.
 
   Returns (d_gates_fwd, d_tokens_fwd, d_gates_bwd, d_tokens_bwd).
   """
-  grad_fwd = grad_fwd.contiguous()
-  grad_bwd = grad_bwd.contiguous()
-  d_tokens_fwd = torch.empty_like(grad_fwd)
+  d_tokens_fwd = torch.empty_like(states_fwd)
   d_gates_fwd = torch.empty_like(gates_fwd)
-  d_tokens_bwd = torch.empty_like(grad_bwd)
+  d_tokens_bwd = torch.empty_like(states_bwd)
   d_gates_bwd = torch.empty_like(gates_bwd)
-  _ops.scan_bidi_bwd(grad_fwd, grad_bwd, gates_fwd, gates_bwd, states_fwd,
-                     states_bwd, d_tokens_fwd, d_gates_fwd, d_tokens_bwd,
-                     d_gates_bwd, cu_seqlens, num_channels=no_channels)
+  _ops.scan_bidi_bwd_any(grad_fwd, grad_bwd, gates_fwd, gates_bwd,
+                         states_fwd, states_bwd, d_tokens_fwd, d_gates_fwd,
+                         d_tokens_bwd, d_gates_bwd, cu_seqlens,
+                         num_channels=no_channels)
   return d_gates_fwd, d_tokens_fwd, d_gates_bwd, d_tokens_bwd
 
 
 @scan_bidi_bwd_op.register_fake
 def _(grad_fwd, grad_bwd, states_fwd, states_bwd, gates_fwd, gates_bwd,
       cu_seqlens, num_chunks, no_channels, chunk_size):
-  cf = torch.contiguous_format
-  return (torch.empty_like(gates_fwd),
-          torch.empty_like(grad_fwd, memory_format=cf),
-          torch.empty_like(gates_bwd),
-          torch.empty_like(grad_bwd, memory_format=cf))
+  return (torch.empty_like(gates_fwd), torch.empty_like(states_fwd),
+          torch.empty_like(gates_bwd), torch.empty_like(states_bwd))
 
 
 def _scan_bidi_setup_context(ctx, inputs, output) -> None:
@@ -181,10 +178,12 @@ def _scan_bidi_setup_context(ctx, inputs, output) -> None:
 
 def _scan_bidi_backward(ctx, grad_fwd, grad_bwd):
   states_fwd, states_bwd, gates_fwd, gates_bwd = ctx.saved_tensors
+  # an output without a gradient: a zero gradient constant along time (read
+  # as one value per row by the backward, no [C, T] zeros tensor)
   if grad_fwd is None:
-    grad_fwd = torch.zeros_like(states_fwd)
+    grad_fwd = states_fwd.new_zeros(()).expand_as(states_fwd)
   if grad_bwd is None:
-    grad_bwd = torch.zeros_like(states_bwd)
+    grad_bwd = states_bwd.new_zeros(()).expand_as(states_bwd)
   d_gates_fwd, d_tokens_fwd, d_gates_bwd, d_tokens_bwd = scan_bidi_bwd_op(
     grad_fwd, grad_bwd, states_fwd, states_bwd, gates_fwd, gates_bwd,
     ctx.cu_seqlens, ctx.num_chunks, ctx.no_channels, ctx.chunk_size,

@@ -111,21 +111,24 @@ class ScanBidirectionalBranched(torch.autograd.Function):
       ctx.save_for_backward(
         out_tokens_fwd, out_tokens_bwd, gates_fwd, gates_bwd
       )
+    # an output that receives no gradient arrives as None (a zero gradient
+    # read as one value, not a materialised zeros tensor)
+    ctx.set_materialize_grads(False)
     return out_tokens_fwd, out_tokens_bwd
 
   @staticmethod
   def backward(ctx, grad_output_fwd, grad_output_bwd):
     states_fwd, states_bwd, gates_fwd, gates_bwd = ctx.saved_tensors
-    grad_output_fwd = grad_output_fwd.contiguous()
-    grad_output_bwd = grad_output_bwd.contiguous()
-    d_tokens_fwd = torch.empty_like(grad_output_fwd)
+    # gradients constant along time (out.sum()) are read one value per row;
+    # any other layout is made contiguous, as the reference does
+    d_tokens_fwd = torch.empty_like(states_fwd)
     d_gates_fwd = torch.empty_like(gates_fwd)
-    d_tokens_bwd = torch.empty_like(grad_output_bwd)
+    d_tokens_bwd = torch.empty_like(states_bwd)
     d_gates_bwd = torch.empty_like(gates_bwd)
-    _ops.scan_bidi_bwd(grad_output_fwd, grad_output_bwd, gates_fwd,
-                       gates_bwd, states_fwd, states_bwd, d_tokens_fwd,
-                       d_gates_fwd, d_tokens_bwd, d_gates_bwd,
-                       ctx.cu_seqlens, num_channels=ctx.grid[2])
+    _ops.scan_bidi_bwd_any(grad_output_fwd, grad_output_bwd, gates_fwd,
+                           gates_bwd, states_fwd, states_bwd, d_tokens_fwd,
+                           d_gates_fwd, d_tokens_bwd, d_gates_bwd,
+                           ctx.cu_seqlens, num_channels=ctx.grid[2])
     return (
       d_gates_fwd,
       d_tokens_fwd,

@@ -658,14 +658,15 @@ struct FwdParams {
 struct BwdParams {
   Geometry geo;
   BwdPtrs br[2];
-  int64_t dy_rs;  // DYC: element stride between rows of the gradient
+  int64_t dy_rs[2];  // DYC: element stride between rows of each gradient
 };
 
-// DYC: the gradient of row c is the one value dy[c * dy_rs] (unshifted dy).
+// DYC: the gradient of row c of branch br is the one value
+// dy[c * dy_rs[br]] (unshifted dy).
 template <class IO, bool DYC>
 __device__ inline float dyc_value(const BwdParams& p, int br, int64_t row) {
   if (!DYC) return 0.0f;
-  return IO::load1(p.br[br].dy + row * p.dy_rs * IO::ES);
+  return IO::load1(p.br[br].dy + row * p.dy_rs[br] * IO::ES);
 }
 
 

@@ -93,20 +93,22 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
   return item_fwd(p, dtype, dirs, aln, wa, stream);
 }
 
-// dyc: dy[0] holds one gradient value per row (element stride dy_rs between
-// rows) that is constant along time; single-branch calls only.
+// dyc: dy[b] holds one gradient value per row (element stride dy_rs[b]
+// between rows) that is constant along time.
 int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
             void* const* dx, void* const* dg, int nbranch, int dirs,
             const void* cu, int cu_dtype, int64_t S, int64_t C, int64_t T,
             int dtype, void* ws, int64_t ws_bytes, void* stream,
-            bool dyc = false, int64_t dy_rs = 0) {
+            bool dyc = false, const int64_t* dy_rs = nullptr) {
   int st = check_geometry(cu, cu_dtype, S, C, T, dtype);
   if (st) return st;
   for (int b = 0; b < nbranch; ++b)
     if (!dy[b] || !g[b] || !h[b] || !dx[b] || !dg[b]) return ASC_E_NULL;
   const int es = elem_size(dtype);
   const int v = 16 / es;
-  if (dyc && (nbranch != 1 || dy_rs < 0)) return ASC_E_ARG;
+  if (dyc)
+    for (int b = 0; b < nbranch; ++b)
+      if (dy_rs[b] < 0) return ASC_E_ARG;
   const void* all[10];
   int n = 0;
   for (int b = 0; b < nbranch; ++b) {
@@ -136,7 +138,7 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
     p.br[b].dg = static_cast<char*>(dg[b]) - shift;
     p.br[b].pend = p.geo.phase + C * T;
   }
-  p.dy_rs = dy_rs;
+  for (int b = 0; b < nbranch; ++b) p.dy_rs[b] = dyc ? dy_rs[b] : 0;
   if (!dyc && lb_use(S, C, T, nbranch, v) &&
       lb_bwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st))
     return st;
@@ -225,10 +227,11 @@ int asc_scan_bwd_rowgrad(const void* grad_rows, int64_t grad_row_stride,
   const void* h[1] = {states};
   void* dx[1] = {d_tokens};
   void* dg[1] = {d_gates};
+  const int64_t rs[1] = {grad_row_stride};
   if (grad_row_stride < 0) return ASC_E_ARG;
   return run_bwd(dy, g, h, dx, dg, 1, causal ? 1 : 2, cu_seqlens, cu_dtype,
                  num_seq, num_channels, seq_stride, dtype, nullptr, 0, stream,
-                 true, grad_row_stride);
+                 true, rs);
 }
 
 int asc_scan_bidi_fwd(const void* gates_fwd, const void* tokens_fwd,
@@ -261,6 +264,25 @@ int asc_scan_bidi_bwd(const void* grad_fwd, const void* grad_bwd,
   return run_bwd(dy, g, h, dx, dg, 2, 3, cu_seqlens, cu_dtype, num_seq,
                  num_channels, seq_stride, dtype, workspace, workspace_bytes,
                  stream);
+}
+
+int asc_scan_bidi_bwd_rowgrad(
+    const void* grad_fwd_rows, int64_t grad_fwd_row_stride,
+    const void* grad_bwd_rows, int64_t grad_bwd_row_stride,
+    const void* gates_fwd, const void* gates_bwd, const void* states_fwd,
+    const void* states_bwd, void* d_tokens_fwd, void* d_gates_fwd,
+    void* d_tokens_bwd, void* d_gates_bwd, const void* cu_seqlens,
+    int cu_dtype, int64_t num_seq, int64_t num_channels, int64_t seq_stride,
+    int dtype, void* stream) {
+  const void* dy[2] = {grad_fwd_rows, grad_bwd_rows};
+  const void* g[2] = {gates_fwd, gates_bwd};
+  const void* h[2] = {states_fwd, states_bwd};
+  void* dx[2] = {d_tokens_fwd, d_tokens_bwd};
+  void* dg[2] = {d_gates_fwd, d_gates_bwd};
+  const int64_t rs[2] = {grad_fwd_row_stride, grad_bwd_row_stride};
+  if (grad_fwd_row_stride < 0 || grad_bwd_row_stride < 0) return ASC_E_ARG;
+  return run_bwd(dy, g, h, dx, dg, 2, 3, cu_seqlens, cu_dtype, num_seq,
+                 num_channels, seq_stride, dtype, nullptr, 0, stream, true, rs);
 }
 
 }  // extern "C"

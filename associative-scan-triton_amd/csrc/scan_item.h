@@ -304,9 +304,10 @@ const void* pick_fwd(int dirs, bool aln, bool wa) {
 template <class IO, int U>
 const void* pick_bwd(int dirs, bool aln, bool dyc) {
 #define ASC_B(D, A, Y) reinterpret_cast<const void*>(&k_scan_bwd<IO, D, A, Y, U>)
-  if (dyc) {  // single-branch calls only
+  if (dyc) {
     if (dirs == 1) return aln ? ASC_B(1, true, true) : ASC_B(1, false, true);
-    return aln ? ASC_B(2, true, true) : ASC_B(2, false, true);
+    if (dirs == 2) return aln ? ASC_B(2, true, true) : ASC_B(2, false, true);
+    return aln ? ASC_B(3, true, true) : ASC_B(3, false, true);
   }
   if (dirs == 1) return aln ? ASC_B(1, true, false) : ASC_B(1, false, false);
   if (dirs == 2) return aln ? ASC_B(2, true, false) : ASC_B(2, false, false);

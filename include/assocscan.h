@@ -184,6 +184,27 @@ int asc_scan_bidi_bwd(const void* grad_fwd, const void* grad_bwd,
                       void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * asc_scan_bidi_bwd for gradients that are constant along time in every
+ * row (as asc_scan_bwd_rowgrad): grad_fwd[c, t] =
+ * grad_fwd_rows[c * grad_fwd_row_stride], and likewise for the reverse
+ * branch.  A stride of 0 with a single zero value stands for a branch whose
+ * output received no gradient.  Runs the workspace-free walks.
+ *
+ * Replaces: scan_eager.py:160-169 and scan_compiled.py:262-277 when both
+ *   incoming gradients are expanded (stride-0 in time) tensors, which the
+ *   reference materialises with .contiguous() (scan_eager.py:161,166;
+ *   scan_compiled.py:262-263).
+ */
+int asc_scan_bidi_bwd_rowgrad(
+    const void* grad_fwd_rows, int64_t grad_fwd_row_stride,
+    const void* grad_bwd_rows, int64_t grad_bwd_row_stride,
+    const void* gates_fwd, const void* gates_bwd, const void* states_fwd,
+    const void* states_bwd, void* d_tokens_fwd, void* d_gates_fwd,
+    void* d_tokens_bwd, void* d_gates_bwd, const void* cu_seqlens,
+    int cu_dtype, int64_t num_seq, int64_t num_channels, int64_t seq_stride,
+    int dtype, void* stream);
+
+/*
  * Segment-aware shift by one position with padding, on a contiguous
  * [num_channels, seq_len] tensor.
  *   backward = 1: out[:, p] = data[:, p-1], pad at every segment start

@@ -119,3 +119,23 @@ def test_rowgrad_validation_codes():
   assert call(dtype=5) == -2
   assert call(grad=6) == -4       # fp32 gradient not 4-byte aligned
   assert call(S=0) == 0           # empty: nothing launched
+
+
+def test_bidi_rowgrad_validation_codes():
+  lib = _lib.load()
+  base = [8, 0, 8, 0] + [8] * 9 + [0, 1, 1, 4, 0, None]
+
+  def call(i=None, v=None):
+    a = list(base)
+    if i is not None:
+      a[i] = v
+    return lib.asc_scan_bidi_bwd_rowgrad(*a)
+
+  assert call(0, None) == -1      # forward-branch gradient
+  assert call(2, None) == -1      # reverse-branch gradient
+  assert call(12, None) == -1     # cu_seqlens
+  assert call(1, -1) == -5        # negative row stride
+  assert call(3, -2) == -5
+  assert call(17, 9) == -2        # dtype
+  assert call(2, 6) == -4         # fp32 gradient not 4-byte aligned
+  assert call(14, 0) == 0         # num_seq = 0: nothing launched

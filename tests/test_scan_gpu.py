@@ -729,6 +729,91 @@ def test_rowgrad_entry_point(dtype, causal):
     check_close(dg, dg_ref, dtype, "dg")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+def test_bidi_rowgrad_entry_point(dtype):
+  """asc_scan_bidi_bwd_rowgrad directly: per-row values with different
+  strides per branch (3 and 0), every walk; matches the dense entry point
+  bit for bit (both run the workspace-free walks) and the oracle."""
+  from associative_scan_triton import _ops
+  prev = _ops.USE_WORKSPACE
+  _ops.USE_WORKSPACE = False
+  try:
+    for lens, C in (([70000, 5, 33000], 70), ([900, 1, 2, 4096], 100)):
+      gf, hf = make(lens, C, dtype, seed=1, n=2, glo=0.5)
+      gb, hb = make(lens, C, dtype, seed=2, n=2, glo=0.5)
+      rows = torch.randn(C, 3, generator=torch.Generator().manual_seed(5)).to(dtype)
+      one = torch.randn(1, generator=torch.Generator().manual_seed(6)).to(dtype)
+      T = sum(lens)
+      cu = torch.tensor(cu_of(lens), device=DEV)
+      d = [t.to(DEV) for t in (gf, gb, hf, hb)]
+      outs = [torch.empty(C, T, dtype=dtype, device=DEV) for _ in range(4)]
+      rd, od = rows.to(DEV), one.to(DEV)
+      _ops.scan_bidi_bwd_rowgrad(rd[:, 1], 3, od, 0, *d, *outs, cu)
+      dyf = rows[:, 1:2].expand(C, T)
+      dyb = one.reshape(1, 1).expand(C, T)
+      dense = [torch.empty_like(o) for o in outs]
+      _ops.scan_bidi_bwd(dyf.contiguous().to(DEV), dyb.contiguous().to(DEV),
+                         *d, *dense, cu)
+      for a, b in zip(outs, dense):
+        assert torch.equal(a, b)
+      dxf, dgf = oracle.scan_bwd(npf(dyf), npf(gf), npf(hf), cu_of(lens), True)
+      dxb, dgb = oracle.scan_bwd(npf(dyb), npf(gb), npf(hb), cu_of(lens), False)
+      check_close(outs[0], dxf, dtype, "dx fwd")
+      check_close(outs[1], dgf, dtype, "dg fwd")
+      check_close(outs[2], dxb, dtype, "dx bwd")
+      check_close(outs[3], dgb, dtype, "dg bwd")
+  finally:
+    _ops.USE_WORKSPACE = prev
+
+
+@pytest.mark.parametrize("compiled", [False, True], ids=["eager", "compiled"])
+@pytest.mark.parametrize("use", ["both", "fwd-only", "bwd-only", "mixed"])
+def test_bidi_time_constant_gradients(compiled, use):
+  """Bidirectional API with gradients that are constant along time
+  (out.sum()), with one branch unused (its gradient is None), and with one
+  dense gradient: every combination matches the materialised gradients bit
+  for bit and the oracle."""
+  lens, C, dtype = [3000, 17, 5000], 80, torch.float32
+  fn = (ast.scan_bidirectional_branched_compiled if compiled
+        else ast.scan_bidirectional_branched)
+  gf, xf = make(lens, C, dtype, seed=1, n=2, glo=0.5)
+  gb, xb = make(lens, C, dtype, seed=2, n=2, glo=0.5)
+  T = sum(lens)
+  args = grid_args(lens, C)
+  dense_b = torch.rand(C, T, generator=torch.Generator().manual_seed(9)).to(DEV)
+
+  def run(loss_of):
+    ts = [t.to(DEV).requires_grad_(True) for t in (gf, xf, gb, xb)]
+    yf, yb = fn(*ts, args)
+    loss_of(yf, yb)
+    return (yf.detach(), yb.detach()), [t.grad for t in ts]
+
+  ones = torch.ones(C, T, device=DEV)
+  zeros = torch.zeros(C, T, device=DEV)
+  losses = {
+    "both": (lambda yf, yb: (yf.sum() + yb.sum()).backward(), ones, ones),
+    "fwd-only": (lambda yf, yb: yf.sum().backward(), ones, zeros),
+    "bwd-only": (lambda yf, yb: yb.sum().backward(), zeros, ones),
+    "mixed": (lambda yf, yb: (yf.sum() + (yb * dense_b).sum()).backward(),
+              ones, dense_b),
+  }
+  loss_of, dyf, dyb = losses[use]
+  (yf, yb), got = run(loss_of)
+  _, ref = run(lambda a, b: torch.autograd.backward([a, b], [dyf, dyb]))
+  from associative_scan_triton import _lib
+  lookback = _lib.load().asc_scan_workspace_bytes(
+    len(lens), C, T, _lib.dtype_code(gf), 2) > 0
+  assert not lookback
+  for a, b in zip(got, ref):
+    assert torch.equal(a, b)
+  dxf, dgf = oracle_bwd(dyf.cpu(), gf, npf(yf), lens, causal=True)
+  dxb, dgb = oracle_bwd(dyb.cpu(), gb, npf(yb), lens, causal=False)
+  check_close(got[0], dgf, dtype, "dg fwd")
+  check_close(got[1], dxf, dtype, "dx fwd")
+  check_close(got[2], dgb, dtype, "dg bwd")
+  check_close(got[3], dxb, dtype, "dx bwd")
+
+
 # ---------------------------------------------------------------------------
 # HIP graph capture
 # ---------------------------------------------------------------------------
