@@ -17,7 +17,7 @@ from associative_scan_triton._build import LIB_PATH
 
 ASC_F32, ASC_F16, ASC_BF16 = 0, 1, 2
 ASC_CU_I32, ASC_CU_I64 = 0, 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _DTYPES = {
   torch.float32: ASC_F32,
@@ -36,16 +36,21 @@ _U = ctypes.c_uint
 SIGNATURES = {
   "asc_abi_version": [],
   "asc_scan_workspace_bytes": [_L, _L, _L, _I, _I],
+  "asc_scan_workspace_walk": [_L, _L, _L, _I, _I],
   "asc_set_lookback_spin_limit": [_U],
   "asc_strerror": [_I],
   "asc_scan_fwd": [_P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P, _L, _P],
   "asc_scan_bwd": [_P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P, _L, _P],
-  "asc_scan_bwd_rowgrad": [_P, _L, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P],
+  "asc_scan_bwd_rowgrad": [_P, _L, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P, _L, _P],
   "asc_scan_bidi_fwd": [_P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _P, _L, _P],
   "asc_scan_bidi_bwd": [_P] * 11 + [_I, _L, _L, _L, _I, _P, _L, _P],
-  "asc_scan_bidi_bwd_rowgrad": [_P, _L, _P, _L] + [_P] * 9 + [_I, _L, _L, _L, _I, _P],
+  "asc_scan_bidi_bwd_rowgrad": [_P, _L, _P, _L] + [_P] * 9 + [_I, _L, _L, _L, _I, _P, _L, _P],
   "asc_shift_pad": [_P, _P, _P, _I, _L, _L, _L, _I, _D, _I, _I, _P],
 }
+# walks a workspace buys (asc_scan_workspace_walk)
+WALK_LOOKBACK = 1
+WALK_CHAINED = 2
+
 RESTYPES = {
   "asc_strerror": ctypes.c_char_p,
   "asc_scan_workspace_bytes": ctypes.c_int64,

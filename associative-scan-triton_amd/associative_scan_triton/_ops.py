@@ -163,10 +163,11 @@ def scan_bwd_rowgrad(grad: torch.Tensor, row_stride: int, gates: torch.Tensor,
   cu = cu.contiguous()
   S, C, T = _geometry(states, cu, num_channels)
   with _OnDevice(dev):
+    ws, nb = _workspace(lib, dev, S, C, T, dt, 1)
     _lib.check(lib.asc_scan_bwd_rowgrad(
       grad.data_ptr(), int(row_stride), gates.data_ptr(), states.data_ptr(),
       d_tokens.data_ptr(), d_gates.data_ptr(), cu.data_ptr(), cuc, S, C, T,
-      dt, 1 if causal else 0, _lib.stream_of(dev)))
+      dt, 1 if causal else 0, _lib.ptr(ws), nb, _lib.stream_of(dev)))
 
 
 def scan_bwd_any(grad: torch.Tensor, gates: torch.Tensor, states: torch.Tensor,
@@ -175,15 +176,16 @@ def scan_bwd_any(grad: torch.Tensor, gates: torch.Tensor, states: torch.Tensor,
                  num_channels: int | None = None) -> None:
   """Backward for any incoming gradient layout: a gradient that is constant
   along time is read one value per row (no materialised copy) unless the
-  geometry runs the look-back walk; any other layout is made contiguous, as
-  the reference does (scan_eager.py:61)."""
+  geometry runs the look-back walk for few items, which needs the full
+  gradient; any other layout is made contiguous, as the reference does
+  (scan_eager.py:61)."""
   rs = row_constant_stride(grad, states, num_channels)
   if rs is not None:
     lib = _lib.load()
     cu_c = cu.contiguous()
     S, C, T = _geometry(states, cu_c, num_channels)
-    if not USE_WORKSPACE or lib.asc_scan_workspace_bytes(
-        S, C, T, _lib.dtype_code(states), 1) <= 0:
+    if not USE_WORKSPACE or lib.asc_scan_workspace_walk(
+        S, C, T, _lib.dtype_code(states), 1) != _lib.WALK_LOOKBACK:
       scan_bwd_rowgrad(grad, rs, gates, states, d_tokens, d_gates, cu_c,
                        causal, num_channels)
       return
@@ -252,11 +254,12 @@ def scan_bidi_bwd_rowgrad(dyf: torch.Tensor, rsf: int, dyb: torch.Tensor,
   cu = cu.contiguous()
   S, C, T = _geometry(hf, cu, num_channels)
   with _OnDevice(dev):
+    ws, nb = _workspace(lib, dev, S, C, T, dt, 2)
     _lib.check(lib.asc_scan_bidi_bwd_rowgrad(
       dyf.data_ptr(), int(rsf), dyb.data_ptr(), int(rsb), gf.data_ptr(),
       gb.data_ptr(), hf.data_ptr(), hb.data_ptr(), dxf.data_ptr(),
       dgf.data_ptr(), dxb.data_ptr(), dgb.data_ptr(), cu.data_ptr(), cuc, S,
-      C, T, dt, _lib.stream_of(dev)))
+      C, T, dt, _lib.ptr(ws), nb, _lib.stream_of(dev)))
 
 
 def scan_bidi_bwd_any(dyf: torch.Tensor | None, dyb: torch.Tensor | None,
@@ -268,7 +271,7 @@ def scan_bidi_bwd_any(dyf: torch.Tensor | None, dyb: torch.Tensor | None,
   for a branch whose output received no gradient (zero).  When both
   gradients are constant along time (stride-0 expanded tensors, or None)
   they are read one value per row, unless the geometry runs the look-back
-  walk; otherwise both are made contiguous, as the reference does
+  walk for few items; otherwise both are made contiguous, as the reference does
   (scan_eager.py:161,166)."""
   zero = None
   if dyf is None or dyb is None:
@@ -279,8 +282,8 @@ def scan_bidi_bwd_any(dyf: torch.Tensor | None, dyb: torch.Tensor | None,
     lib = _lib.load()
     cu_c = cu.contiguous()
     S, C, T = _geometry(hf, cu_c, num_channels)
-    if not USE_WORKSPACE or lib.asc_scan_workspace_bytes(
-        S, C, T, _lib.dtype_code(hf), 2) <= 0:
+    if not USE_WORKSPACE or lib.asc_scan_workspace_walk(
+        S, C, T, _lib.dtype_code(hf), 2) != _lib.WALK_LOOKBACK:
       scan_bidi_bwd_rowgrad(zero if dyf is None else dyf, rsf,
                             zero if dyb is None else dyb, rsb, gf, gb, hf, hb,
                             dxf, dgf, dxb, dgb, cu_c, num_channels)

@@ -650,16 +650,25 @@ __device__ inline int wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
 }
 
+// skip: nullptr, or a flag in device memory that, when set, makes every
+// workgroup return at once (the chained walk ran instead; see scan_chain.hip).
 struct FwdParams {
   Geometry geo;
   FwdPtrs br[2];
+  const uint32_t* skip;
 };
 
 struct BwdParams {
   Geometry geo;
   BwdPtrs br[2];
   int64_t dy_rs[2];  // DYC: element stride between rows of each gradient
+  const uint32_t* skip;
 };
+
+template <class Params>
+__device__ inline bool skipped(const Params& p) {
+  return p.skip != nullptr && *p.skip != 0u;
+}
 
 // DYC: the gradient of row c of branch br is the one value
 // dy[c * dy_rs[br]] (unshifted dy).
@@ -753,10 +762,28 @@ int wg_bwd(BwdParams p, int nw, int dtype, int dirs, bool aln, bool dyc,
 bool lb_use(int64_t S, int64_t C, int64_t T, int nbranch, int v);
 int64_t lb_bytes(int64_t n, int v, int nbranch);
 unsigned lb_set_spin_limit(unsigned polls);
+unsigned lb_spin_limit();
+// Zeroes `bytes` (a multiple of 8) of a workspace with a kernel on `stream`.
+int fill_zero(void* ws, int64_t bytes, void* stream);
 bool lb_fwd(const FwdParams& p, int dtype, int dirs, bool aln, void* ws,
             int64_t ws_bytes, void* stream, int& status);
 bool lb_bwd(const BwdParams& p, int dtype, int dirs, bool aln, void* ws,
             int64_t ws_bytes, void* stream, int& status);
+
+// scan_chain.hip: chained chunks for segments aligned to the chunk size.
+// chain_bytes: its workspace (0 when the geometry cannot use it).
+// chain_fwd / chain_bwd return false (nothing launched) when the workspace is
+// missing or too small; otherwise they launch the chained walk, which checks
+// cu_seqlens on the device and runs only when every segment edge is
+// chunk-aligned, and set *skip to a device flag that is nonzero exactly
+// when it ran: the caller then launches its usual walk with that flag.
+int64_t chain_bytes(int64_t S, int64_t C, int64_t T, int v, int nbranch);
+bool chain_fwd(const FwdParams& p, int dtype, bool aln, int dirs, void* ws,
+               int64_t ws_bytes, void* stream, int& status,
+               const uint32_t** skip);
+bool chain_bwd(const BwdParams& p, int dtype, bool aln, bool dyc, int dirs,
+               void* ws, int64_t ws_bytes, void* stream, int& status,
+               const uint32_t** skip);
 
 }  // namespace asc
 

@@ -83,11 +83,15 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
     p.br[b].pend = p.geo.phase + C * T;
   }
   const bool wa = a != nullptr;
-  // the look-back walk does not write the gate product; it needs the
+  // the look-back walks do not write the gate product; they need the
   // caller's workspace (else the per-item walks run)
-  if (!wa && lb_use(S, C, T, nbranch, v) &&
-      lb_fwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st))
-    return st;
+  if (!wa && lb_use(S, C, T, nbranch, v)) {
+    if (lb_fwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st)) return st;
+  } else if (!wa && chain_fwd(p, dtype, aln, dirs, ws, ws_bytes, stream, st,
+                              &p.skip)) {
+    // the per-item walk below runs only if cu_seqlens turns out unaligned
+    if (st) return st;
+  }
   const int nw = wa ? 0 : pick_walk(S, C, T, nbranch, v, false);
   if (nw) return wg_fwd(p, nw, dtype, dirs, aln, stream);
   return item_fwd(p, dtype, dirs, aln, wa, stream);
@@ -139,9 +143,13 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
     p.br[b].pend = p.geo.phase + C * T;
   }
   for (int b = 0; b < nbranch; ++b) p.dy_rs[b] = dyc ? dy_rs[b] : 0;
-  if (!dyc && lb_use(S, C, T, nbranch, v) &&
-      lb_bwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st))
-    return st;
+  if (!dyc && lb_use(S, C, T, nbranch, v)) {
+    if (lb_bwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st)) return st;
+  } else if (chain_bwd(p, dtype, aln, dyc, dirs, ws, ws_bytes, stream, st,
+                       &p.skip)) {
+    // the per-item walk below runs only if cu_seqlens turns out unaligned
+    if (st) return st;
+  }
   const int nw = pick_walk(S, C, T, nbranch, v, true);
   if (nw) return wg_bwd(p, nw, dtype, dirs, aln, dyc, stream);
   return item_bwd(p, dtype, dirs, aln, dyc, stream);
@@ -166,8 +174,20 @@ int64_t asc_scan_workspace_bytes(int64_t num_seq, int64_t num_channels,
     return ASC_E_ARG;
   if (num_channels > 0 && seq_stride > (INT64_MAX / 64) / num_channels)
     return ASC_E_SIZE;
-  if (!lb_use(num_seq, num_channels, seq_stride, nbranch, 16 / es)) return 0;
-  return lb_bytes(num_channels * seq_stride, 16 / es, nbranch);
+  if (lb_use(num_seq, num_channels, seq_stride, nbranch, 16 / es))
+    return lb_bytes(num_channels * seq_stride, 16 / es, nbranch);
+  return chain_bytes(num_seq, num_channels, seq_stride, 16 / es, nbranch);
+}
+
+int asc_scan_workspace_walk(int64_t num_seq, int64_t num_channels,
+                            int64_t seq_stride, int dtype, int nbranch) {
+  const int64_t nb = asc_scan_workspace_bytes(num_seq, num_channels,
+                                              seq_stride, dtype, nbranch);
+  if (nb <= 0) return static_cast<int>(nb);
+  return lb_use(num_seq, num_channels, seq_stride, nbranch,
+                16 / elem_size(dtype))
+             ? ASC_WALK_LOOKBACK
+             : ASC_WALK_CHAINED;
 }
 
 unsigned asc_set_lookback_spin_limit(unsigned polls) {
@@ -221,6 +241,7 @@ int asc_scan_bwd_rowgrad(const void* grad_rows, int64_t grad_row_stride,
                          void* d_gates, const void* cu_seqlens, int cu_dtype,
                          int64_t num_seq, int64_t num_channels,
                          int64_t seq_stride, int dtype, int causal,
+                         void* workspace, int64_t workspace_bytes,
                          void* stream) {
   const void* dy[1] = {grad_rows};
   const void* g[1] = {gates};
@@ -230,8 +251,8 @@ int asc_scan_bwd_rowgrad(const void* grad_rows, int64_t grad_row_stride,
   const int64_t rs[1] = {grad_row_stride};
   if (grad_row_stride < 0) return ASC_E_ARG;
   return run_bwd(dy, g, h, dx, dg, 1, causal ? 1 : 2, cu_seqlens, cu_dtype,
-                 num_seq, num_channels, seq_stride, dtype, nullptr, 0, stream,
-                 true, rs);
+                 num_seq, num_channels, seq_stride, dtype, workspace,
+                 workspace_bytes, stream, true, rs);
 }
 
 int asc_scan_bidi_fwd(const void* gates_fwd, const void* tokens_fwd,
@@ -273,7 +294,7 @@ int asc_scan_bidi_bwd_rowgrad(
     const void* states_bwd, void* d_tokens_fwd, void* d_gates_fwd,
     void* d_tokens_bwd, void* d_gates_bwd, const void* cu_seqlens,
     int cu_dtype, int64_t num_seq, int64_t num_channels, int64_t seq_stride,
-    int dtype, void* stream) {
+    int dtype, void* workspace, int64_t workspace_bytes, void* stream) {
   const void* dy[2] = {grad_fwd_rows, grad_bwd_rows};
   const void* g[2] = {gates_fwd, gates_bwd};
   const void* h[2] = {states_fwd, states_bwd};
@@ -282,7 +303,8 @@ int asc_scan_bidi_bwd_rowgrad(
   const int64_t rs[2] = {grad_fwd_row_stride, grad_bwd_row_stride};
   if (grad_fwd_row_stride < 0 || grad_bwd_row_stride < 0) return ASC_E_ARG;
   return run_bwd(dy, g, h, dx, dg, 2, 3, cu_seqlens, cu_dtype, num_seq,
-                 num_channels, seq_stride, dtype, nullptr, 0, stream, true, rs);
+                 num_channels, seq_stride, dtype, workspace, workspace_bytes,
+                 stream, true, rs);
 }
 
 }  // extern "C"

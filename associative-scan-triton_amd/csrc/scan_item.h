@@ -247,6 +247,7 @@ __device__ void bwd_item(const BwdPtrs& t, int64_t P0, int64_t P1, int lane,
 // occupancy).
 template <class IO, int DIRS, bool ALN, bool WA, int U>
 __global__ void __launch_bounds__(kWPB* kWave) k_scan_fwd(FwdParams p) {
+  if (skipped(p)) return;
   const int lane = threadIdx.x % kWave;
   const int64_t W = p.geo.items * p.geo.nbranch;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kWPB;
@@ -268,6 +269,7 @@ __global__ void __launch_bounds__(kWPB* kWave) k_scan_fwd(FwdParams p) {
 // 3 = branch 0 causal / branch 1 reverse.
 template <class IO, int DIRS, bool ALN, bool DYC, int U>
 __global__ void __launch_bounds__(kWPB* kWave) k_scan_bwd(BwdParams p) {
+  if (skipped(p)) return;
   const int lane = threadIdx.x % kWave;
   const int64_t W = p.geo.items * p.geo.nbranch;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kWPB;

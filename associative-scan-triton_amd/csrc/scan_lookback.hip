@@ -1,4 +1,5 @@
 #include "asc_common.h"
+#include "lookback_slots.h"
 
 namespace asc {
 namespace {
@@ -62,38 +63,6 @@ constexpr int kLbWaves = ASC_LB_WAVES;  // parts (waves) per workgroup tile
 // Elements per part for v elements per vector (host side; matches LbU).
 constexpr int64_t lb_part_elems(int v) {
   return v == 4 ? 256 * ASC_LB_U_F32 : 2 * 512;
-}
-
-typedef unsigned long long u64;
-// One carry slot per tile, two tagged words: x holds (status << 32 | value)
-// with status kLbAgg (the tile's aggregate X) or kLbIncl (its inclusive
-// value, the state after the tile); a holds (kLbAgg << 32 | A).  Each word is
-// read and written whole, so a reader never sees a value without its tag.
-struct LbSlot {
-  u64 x, a;
-};
-enum : uint32_t { kLbNone = 0, kLbAgg = 1, kLbIncl = 2 };
-
-__device__ inline void lb_put(u64* p, uint32_t st, float v) {
-  const u64 w = (static_cast<u64>(st) << 32) | __float_as_uint(v);
-  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline u64 lb_get(u64* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline uint32_t lb_status(u64 w) { return static_cast<uint32_t>(w >> 32); }
-__device__ inline float lb_value(u64 w) {
-  return __uint_as_float(static_cast<uint32_t>(w));
-}
-// Both words of a slot in one round trip; returns the slot's kind.
-__device__ inline int lb_read(LbSlot* s, float& a, float& x) {
-  const u64 wx = lb_get(&s->x);
-  const u64 wa = lb_get(&s->a);
-  x = lb_value(wx);
-  a = lb_value(wa);
-  const uint32_t sx = lb_status(wx);
-  if (sx == kLbIncl) return kLbIncl;
-  return (sx == kLbAgg && lb_status(wa) == kLbAgg) ? kLbAgg : kLbNone;
 }
 
 struct LbGeo {
@@ -975,19 +944,6 @@ int64_t lb_ntiles(int64_t n, int phase, int v) {
   return (phase + n + te - 1) / te;
 }
 
-int fill_zero(void* ws, int64_t bytes, void* stream) {
-  const int64_t words = bytes / 8;
-  int64_t blocks = (words + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  if (blocks < 1) blocks = 1;
-  u64* p = static_cast<u64*>(ws);
-  int64_t n = words;
-  void* args[] = {&p, &n};
-  const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&k_fill_zero),
-                                       dim3(static_cast<unsigned>(blocks)), dim3(256),
-                                       args, 0, static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? ASC_OK : static_cast<int>(e);
-}
 
 template <class IO>
 const void* pick_fwd_lb(int dirs, bool aln) {
@@ -1022,6 +978,20 @@ bool lb_prepare(const Geometry& geo, int v, void* ws, int64_t ws_bytes,
 
 }  // namespace
 
+int fill_zero(void* ws, int64_t bytes, void* stream) {
+  const int64_t words = bytes / 8;
+  int64_t blocks = (words + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  u64* p = static_cast<u64*>(ws);
+  int64_t n = words;
+  void* args[] = {&p, &n};
+  const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&k_fill_zero),
+                                       dim3(static_cast<unsigned>(blocks)), dim3(256),
+                                       args, 0, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ASC_OK : static_cast<int>(e);
+}
+
 // Walk choice: the look-back walk for problems with few (segment, channel)
 // items (each item of the other walks is one wave or one workgroup, which
 // leaves most CUs idle), the per-item walks otherwise.  Measured on MI355X
@@ -1049,6 +1019,8 @@ bool lb_use(int64_t S, int64_t C, int64_t T, int nbranch, int v) {
 int64_t lb_bytes(int64_t n, int v, int nbranch) {
   return lb_ntiles(n, v - 1, v) * nbranch * static_cast<int64_t>(sizeof(LbSlot));
 }
+
+unsigned lb_spin_limit() { return g_spin_limit; }
 
 unsigned lb_set_spin_limit(unsigned polls) {
   const unsigned prev = g_spin_limit;

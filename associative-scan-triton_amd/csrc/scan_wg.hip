@@ -222,6 +222,7 @@ __device__ void bwd_item_wg(const BwdPtrs& t, int64_t P0, int64_t P1,
 // BLK: item order in channel blocks (item_range).
 template <class IO, int DIRS, bool ALN, int NW, bool BLK>
 __global__ void __launch_bounds__(NW* kWave) k_scan_fwd_wg(FwdParams p) {
+  if (skipped(p)) return;
   __shared__ float2 agg[2 * NW];
   const int lane = threadIdx.x % kWave;
   const int wv = wave_id();
@@ -241,6 +242,7 @@ __global__ void __launch_bounds__(NW* kWave) k_scan_fwd_wg(FwdParams p) {
 
 template <class IO, int DIRS, bool ALN, int NW, bool DYC, bool BLK>
 __global__ void __launch_bounds__(NW* kWave) k_scan_bwd_wg(BwdParams p) {
+  if (skipped(p)) return;
   __shared__ float2 agg[2 * NW];
   const int lane = threadIdx.x % kWave;
   const int wv = wave_id();

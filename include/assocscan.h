@@ -65,7 +65,7 @@ enum {
 };
 
 /* ABI version of this header; bumped on any signature change. */
-#define ASC_ABI_VERSION 2
+#define ASC_ABI_VERSION 3
 int asc_abi_version(void);
 
 /*
@@ -78,6 +78,19 @@ int asc_abi_version(void);
  */
 int64_t asc_scan_workspace_bytes(int64_t num_seq, int64_t num_channels,
                                  int64_t seq_stride, int dtype, int nbranch);
+
+/*
+ * Which walk a workspace of asc_scan_workspace_bytes() buys for this
+ * geometry: 0 = none (the workspace-free walks run), ASC_WALK_LOOKBACK (few
+ * items; any cu_seqlens), ASC_WALK_CHAINED (long segments; runs when every
+ * edge in cu_seqlens is a multiple of the chunk size -- 4096 fp32 / 8192
+ * fp16-bf16 elements -- checked on the device, else the workspace-free walks
+ * run), or a negative ASC_E_* code.  The row-gradient entry points below
+ * cannot use the look-back walk.  No reference counterpart.
+ */
+enum { ASC_WALK_LOOKBACK = 1, ASC_WALK_CHAINED = 2 };
+int asc_scan_workspace_walk(int64_t num_seq, int64_t num_channels,
+                            int64_t seq_stride, int dtype, int nbranch);
 
 /*
  * Test hook, no reference counterpart: sets how many times a look-back wave
@@ -139,7 +152,9 @@ int asc_scan_bwd(const void* grad, const void* gates, const void* states,
  * gradient of out.sum() (or of any loss that reduces over time first), which
  * PyTorch hands over as a stride-0 expanded tensor.  The kernels read one
  * value per row instead of a [C, T] tensor: 4 of the 5 tensors' traffic, and
- * no materialised copy.  Runs the workspace-free walks.
+ * no materialised copy.  The workspace is used as by asc_scan_bwd, except
+ * that the look-back walk for few items does not take this form of the
+ * gradient (those calls run the workspace-free walks).
  *
  * Replaces: scan_eager.py:58-63 (grad_output.contiguous() followed by
  *   backward_scan_fused_full) and scan_compiled.py:158-166 when the incoming
@@ -150,6 +165,7 @@ int asc_scan_bwd_rowgrad(const void* grad_rows, int64_t grad_row_stride,
                          void* d_gates, const void* cu_seqlens, int cu_dtype,
                          int64_t num_seq, int64_t num_channels,
                          int64_t seq_stride, int dtype, int causal,
+                         void* workspace, int64_t workspace_bytes,
                          void* stream);
 
 /*
@@ -188,7 +204,8 @@ int asc_scan_bidi_bwd(const void* grad_fwd, const void* grad_bwd,
  * row (as asc_scan_bwd_rowgrad): grad_fwd[c, t] =
  * grad_fwd_rows[c * grad_fwd_row_stride], and likewise for the reverse
  * branch.  A stride of 0 with a single zero value stands for a branch whose
- * output received no gradient.  Runs the workspace-free walks.
+ * output received no gradient.  The workspace is used as by
+ * asc_scan_bidi_bwd.
  *
  * Replaces: scan_eager.py:160-169 and scan_compiled.py:262-277 when both
  *   incoming gradients are expanded (stride-0 in time) tensors, which the
@@ -202,7 +219,7 @@ int asc_scan_bidi_bwd_rowgrad(
     const void* states_bwd, void* d_tokens_fwd, void* d_gates_fwd,
     void* d_tokens_bwd, void* d_gates_bwd, const void* cu_seqlens,
     int cu_dtype, int64_t num_seq, int64_t num_channels, int64_t seq_stride,
-    int dtype, void* stream);
+    int dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Segment-aware shift by one position with padding, on a contiguous

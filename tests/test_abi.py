@@ -39,7 +39,7 @@ def test_exports_every_declared_symbol():
 
 def test_abi_version_and_strerror():
   lib = _lib.load()
-  assert lib.asc_abi_version() == 2
+  assert lib.asc_abi_version() == 3
   assert lib.asc_strerror(0) == b"success"
   for code in (-1, -2, -3, -4, -5):
     assert lib.asc_strerror(code) and lib.asc_strerror(code) != b"unknown error"
@@ -80,13 +80,21 @@ def test_workspace_bytes():
   b2 = lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 0, 2)
   assert b1 == 16 * -(-(n + 3) // 16384) and b2 == 2 * b1
   assert lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 2, 1) == 16 * -(-(n + 7) // 16384)
-  # many items: the workspace-free walks, no workspace (threshold: 128
-  # (segment, channel, branch) items)
-  assert lib.asc_scan_workspace_bytes(8, 1536, 524288, 0, 1) == 0
-  assert lib.asc_scan_workspace_bytes(1, 128, 4096, 0, 1) > 0
-  assert lib.asc_scan_workspace_bytes(1, 129, 4096, 0, 1) == 0
-  assert lib.asc_scan_workspace_bytes(1, 64, 4096, 0, 2) > 0
-  assert lib.asc_scan_workspace_bytes(1, 65, 4096, 0, 2) == 0
+  # many items (more than 128 (segment, channel, branch) items): rows that
+  # are a whole number of chunks (4096 fp32 / 8192 fp16-bf16 elements) with
+  # segments of at least one chunk on average take the chained walk, a
+  # 256-byte flag plus one 16-byte slot per chunk and branch; other
+  # geometries run the workspace-free walks and need none
+  assert lib.asc_scan_workspace_bytes(8, 1536, 524288, 0, 1) == 256 + 16 * 1536 * 128
+  assert lib.asc_scan_workspace_bytes(8, 1536, 131072, 0, 2) == 0   # two branches
+  assert lib.asc_scan_workspace_bytes(1, 1536, 524288, 0, 1) == 0     # 128 chunks
+  assert lib.asc_scan_workspace_bytes(8, 1536, 524288, 2, 1) == 256 + 16 * 1536 * 64
+  assert lib.asc_scan_workspace_bytes(8, 1536, 524289, 0, 1) == 0     # ragged rows
+  assert lib.asc_scan_workspace_bytes(256, 1536, 524288, 0, 1) == 0   # mean 2048
+  assert lib.asc_scan_workspace_bytes(1, 128, 4000, 0, 1) > 0
+  assert lib.asc_scan_workspace_bytes(1, 129, 4000, 0, 1) == 0
+  assert lib.asc_scan_workspace_bytes(1, 64, 4000, 0, 2) > 0
+  assert lib.asc_scan_workspace_bytes(1, 65, 4000, 0, 2) == 0
   assert lib.asc_scan_workspace_bytes(2, 64, 4096, 2, 1) > 0
   assert lib.asc_scan_workspace_bytes(2, 65, 4096, 1, 1) == 0
   # empty problems need nothing; invalid arguments are errors
@@ -94,6 +102,11 @@ def test_workspace_bytes():
   assert lib.asc_scan_workspace_bytes(1, 4, 128, 9, 1) < 0
   assert lib.asc_scan_workspace_bytes(1, 4, 128, 0, 3) < 0
   assert lib.asc_scan_workspace_bytes(-1, 4, 128, 0, 1) < 0
+  walk = lib.asc_scan_workspace_walk
+  assert walk(8, 1536, 524288, 0, 1) == _lib.WALK_CHAINED
+  assert walk(2, 4, 1_000_000, 0, 1) == _lib.WALK_LOOKBACK
+  assert walk(8, 1536, 524289, 0, 1) == 0
+  assert walk(8, 1536, 524288, 9, 1) < 0
   prev = lib.asc_set_lookback_spin_limit(7)
   assert lib.asc_set_lookback_spin_limit(prev) == 7
 
@@ -106,7 +119,8 @@ def test_error_is_raised_with_message():
 def test_rowgrad_validation_codes():
   lib = _lib.load()
   args = dict(grad=8, rs=0, gates=8, states=8, dx=8, dg=8, cu=8, cu_dtype=0,
-              S=1, C=1, T=4, dtype=0, causal=1, stream=None)
+              S=1, C=1, T=4, dtype=0, causal=1, ws=None, ws_bytes=0,
+              stream=None)
 
   def call(**kw):
     a = dict(args)
@@ -123,7 +137,7 @@ def test_rowgrad_validation_codes():
 
 def test_bidi_rowgrad_validation_codes():
   lib = _lib.load()
-  base = [8, 0, 8, 0] + [8] * 9 + [0, 1, 1, 4, 0, None]
+  base = [8, 0, 8, 0] + [8] * 9 + [0, 1, 1, 4, 0, None, 0, None]
 
   def call(i=None, v=None):
     a = list(base)

@@ -815,6 +815,122 @@ def test_bidi_time_constant_gradients(compiled, use):
 
 
 # ---------------------------------------------------------------------------
+# chained-chunk walk (segments aligned to 4096 fp32 / 8192 fp16-bf16
+# elements, more than 128 items)
+# ---------------------------------------------------------------------------
+
+def _chunk(dtype):
+  return 4096 if dtype == torch.float32 else 8192
+
+
+def _chain_case(dtype, lens, C, rows, spin=None):
+  """Forward (both directions) and backward (both) through the library with
+  a workspace; checks rows `rows` against the oracle and returns the device
+  results."""
+  from associative_scan_triton import _lib, _ops
+  lib = _lib.load()
+  T = sum(lens)
+  g, x, dy = make(lens, C, dtype, glo=0.5, n=3)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  gd, xd, dyd = g.to(DEV), x.to(DEV), dy.to(DEV)
+  assert lib.asc_scan_workspace_walk(len(lens), C, T, _lib.dtype_code(gd),
+                                    1) == _lib.WALK_CHAINED
+  prev = lib.asc_set_lookback_spin_limit(spin) if spin is not None else None
+  try:
+    out = {}
+    for rev in (False, True):
+      h = torch.empty_like(gd)
+      _ops.scan_fwd(gd, xd, h, cu, rev)
+      dx, dg = torch.empty_like(gd), torch.empty_like(gd)
+      _ops.scan_bwd(dyd, gd, h, dx, dg, cu, causal=not rev)
+      out[rev] = (h, dx, dg)
+      for r in rows:
+        h_ref = oracle_fwd(g[r:r + 1], x[r:r + 1], lens, reverse=rev)
+        check_close(h[r:r + 1], h_ref, dtype, f"h row {r} rev={rev}")
+        dx_ref, dg_ref = oracle_bwd(dy[r:r + 1], g[r:r + 1], npf(h[r:r + 1]),
+                                    lens, causal=not rev)
+        check_close(dx[r:r + 1], dx_ref, dtype, f"dx row {r} rev={rev}")
+        check_close(dg[r:r + 1], dg_ref, dtype, f"dg row {r} rev={rev}")
+    return out
+  finally:
+    if prev is not None:
+      lib.asc_set_lookback_spin_limit(prev)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+def test_chain_walk_parity_and_reproducible(dtype):
+  """Aligned segments of 1-3 chunks over 130 rows: every row matches the
+  oracle, and a second run gives the same bits (the carries are composed in
+  a fixed order)."""
+  CH = _chunk(dtype)
+  lens = [2 * CH, CH, 3 * CH]
+  a = _chain_case(dtype, lens, 130, rows=range(130))
+  b = _chain_case(dtype, lens, 130, rows=[])
+  for rev in (False, True):
+    for u, v in zip(a[rev], b[rev]):
+      assert torch.equal(u, v)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+def test_chain_walk_unaligned_falls_back(dtype):
+  """Same row width, segment edges off the chunk grid: the device check
+  sends the call to the per-item walks, which must match the oracle."""
+  CH = _chunk(dtype)
+  _chain_case(dtype, [2 * CH + 5, CH - 5, 3 * CH], 130, rows=[0, 77, 129])
+  _chain_case(dtype, [2 * CH, CH, 3 * CH - 1, 1], 130, rows=[0, 129])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16],
+                         ids=["f32", "bf16"])
+def test_chain_walk_checkpoints(dtype):
+  """A segment of 70 chunks crosses the 64-chunk checkpoint (chunks past it
+  take their carry from the checkpoint's inclusive value); an empty segment
+  is skipped."""
+  CH = _chunk(dtype)
+  _chain_case(dtype, [70 * CH, 0, CH], 130, rows=[0, 65, 129])
+  _chain_case(dtype, [3 * CH, 60 * CH, 7 * CH], 129, rows=[3, 128])
+
+
+def test_chain_walk_bounded_wait_fallback():
+  """Spin limit 0: every chunk that finds a predecessor's slot empty scans
+  its segment's prefix itself; results still match the oracle."""
+  CH = 4096
+  _chain_case(torch.float32, [3 * CH, 66 * CH, CH], 130, rows=[0, 64, 129],
+              spin=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16],
+                         ids=["f32", "bf16"])
+def test_bidirectional_aligned_long_segments(dtype):
+  """Both branches with chunk-aligned long segments over 130 rows: the
+  two-branch launches keep the per-item walks (no workspace is asked for)."""
+  from associative_scan_triton import _lib, _ops
+  CH = _chunk(dtype)
+  lens, C = [CH, 2 * CH], 130
+  gf, xf, dyf = make(lens, C, dtype, seed=1, glo=0.5, n=3)
+  gb, xb, dyb = make(lens, C, dtype, seed=2, glo=0.5, n=3)
+  T = sum(lens)
+  assert _lib.load().asc_scan_workspace_bytes(len(lens), C, T,
+                                              _lib.dtype_code(gf), 2) == 0
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  d = [t.to(DEV) for t in (gf, xf, gb, xb, dyf, dyb)]
+  hf, hb = torch.empty_like(d[0]), torch.empty_like(d[0])
+  _ops.scan_bidi_fwd(d[0], d[1], d[2], d[3], hf, hb, cu)
+  outs = [torch.empty_like(d[0]) for _ in range(4)]
+  _ops.scan_bidi_bwd(d[4], d[5], d[0], d[2], hf, hb, *outs, cu)
+  for r in (0, 64, 129):
+    sl = slice(r, r + 1)
+    check_close(hf[sl], oracle_fwd(gf[sl], xf[sl], lens), dtype, "hf")
+    check_close(hb[sl], oracle_fwd(gb[sl], xb[sl], lens, reverse=True), dtype, "hb")
+    dxf, dgf = oracle_bwd(dyf[sl], gf[sl], npf(hf[sl]), lens, causal=True)
+    dxb, dgb = oracle_bwd(dyb[sl], gb[sl], npf(hb[sl]), lens, causal=False)
+    check_close(outs[0][sl], dxf, dtype, "dxf")
+    check_close(outs[1][sl], dgf, dtype, "dgf")
+    check_close(outs[2][sl], dxb, dtype, "dxb")
+    check_close(outs[3][sl], dgb, dtype, "dgb")
+
+
+# ---------------------------------------------------------------------------
 # HIP graph capture
 # ---------------------------------------------------------------------------
 
