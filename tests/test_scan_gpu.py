@@ -934,13 +934,15 @@ def test_bidirectional_aligned_long_segments(dtype):
 # HIP graph capture
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("C,lens", [(2, [5000, 3000]), (80, [700, 300])],
-                         ids=["lookback", "per-item"])
+@pytest.mark.parametrize("C,lens", [(2, [5000, 3000]), (80, [700, 300]),
+                                    (130, [8192, 4096])],
+                         ids=["lookback", "per-item", "chained"])
 def test_graph_capture_replay(C, lens):
-  """Forward + backward captured in one graph (the look-back walk clears its
-  workspace with a kernel, not a memset) and replayed with fresh inputs and
-  eager launches in between; every replay matches the oracle, and the
-  deterministic per-item walks match the eager launch bit for bit."""
+  """Forward + backward captured in one graph (the look-back and chained
+  walks clear their workspace with a kernel, not a memset) and replayed
+  with fresh inputs and eager launches in between; every replay matches the
+  oracle, and the reproducible walks (per-item, chained) match the eager
+  launch bit for bit."""
   from associative_scan_triton import _ops
   T = sum(lens)
   cu = torch.tensor(cu_of(lens), device=DEV)
@@ -968,8 +970,10 @@ def test_graph_capture_replay(C, lens):
   graph = torch.cuda.CUDAGraph()
   with torch.cuda.graph(graph):
     step()
-  lookback = _ops._lib.load().asc_scan_workspace_bytes(len(lens), C, T, 0, 1) > 0
-  assert lookback == (C == 2)
+  from associative_scan_triton import _lib
+  walk = _lib.load().asc_scan_workspace_walk(len(lens), C, T, 0, 1)
+  assert walk == {2: _lib.WALK_LOOKBACK, 80: 0, 130: _lib.WALK_CHAINED}[C]
+  lookback = walk == _lib.WALK_LOOKBACK
   for _ in range(4):
     fresh()
     graph.replay()
