@@ -21,7 +21,8 @@
 //   * a checkpoint publishes its inclusive value once it has its carry.
 // A wait is bounded: after the spin limit the waiting wave scans the
 // segment's prefix before its chunk itself (one sub-tile at a time), so
-// progress never depends on workgroup scheduling.
+// progress never depends on workgroup scheduling (that carry is composed in
+// another order, so only such a pathological wait changes the last bits).
 //
 // The host cannot see cu_seqlens, so a setup kernel checks on the device
 // that every edge is chunk-aligned (and zeroes the slots); the chained walk
