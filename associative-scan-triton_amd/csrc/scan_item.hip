@@ -38,7 +38,7 @@ int item_fwd(FwdParams p, int dtype, int dirs, bool aln, bool wa,
     }
   }
   const int64_t items = p.geo.items * p.geo.nbranch;
-  return launch(fn, (items + kWPB - 1) / kWPB, kWPB, p, stream);
+  return launch(fn, walk_grid(p, (items + kWPB - 1) / kWPB, kWPB), kWPB, p, stream);
 }
 
 int item_bwd(BwdParams p, int dtype, int dirs, bool aln, bool dyc,
@@ -54,7 +54,7 @@ int item_bwd(BwdParams p, int dtype, int dirs, bool aln, bool dyc,
     }
   }
   const int64_t items = p.geo.items * p.geo.nbranch;
-  return launch(fn, (items + kWPB - 1) / kWPB, kWPB, p, stream);
+  return launch(fn, walk_grid(p, (items + kWPB - 1) / kWPB, kWPB), kWPB, p, stream);
 }
 
 }  // namespace asc

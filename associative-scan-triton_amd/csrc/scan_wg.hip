@@ -316,7 +316,7 @@ int wg_fwd(FwdParams p, int nw, int dtype, int dirs, bool aln, void* stream) {
     case ASC_F16: fn = pick_fwd_wg<IoF16>(nw, dirs, aln, blk); break;
     default: fn = pick_fwd_wg<IoBF16>(nw, dirs, aln, blk); break;
   }
-  return launch(fn, p.geo.items * p.geo.nbranch, nw, p, stream);
+  return launch(fn, walk_grid(p, p.geo.items * p.geo.nbranch, nw), nw, p, stream);
 }
 
 int wg_bwd(BwdParams p, int nw, int dtype, int dirs, bool aln, bool dyc,
@@ -328,7 +328,7 @@ int wg_bwd(BwdParams p, int nw, int dtype, int dirs, bool aln, bool dyc,
     case ASC_F16: fn = pick_bwd_wg<IoF16>(nw, dirs, aln, dyc, blk); break;
     default: fn = pick_bwd_wg<IoBF16>(nw, dirs, aln, dyc, blk); break;
   }
-  return launch(fn, p.geo.items * p.geo.nbranch, nw, p, stream);
+  return launch(fn, walk_grid(p, p.geo.items * p.geo.nbranch, nw), nw, p, stream);
 }
 
 }  // namespace asc
