@@ -459,18 +459,17 @@ __global__ void __launch_bounds__(256)
   if (threadIdx.x == 0) *ok = good ? 1u : 0u;
 }
 
+// dirs 1 or 2: a two-branch call launches each branch on its own
 template <class IO>
 const void* pick_fwd_chain(int dirs) {
   if (dirs == 1) return reinterpret_cast<const void*>(&k_scan_fwd_chain<IO, 1>);
-  if (dirs == 2) return reinterpret_cast<const void*>(&k_scan_fwd_chain<IO, 2>);
-  return reinterpret_cast<const void*>(&k_scan_fwd_chain<IO, 3>);
+  return reinterpret_cast<const void*>(&k_scan_fwd_chain<IO, 2>);
 }
 
 template <class IO, bool DYC>
 const void* pick_bwd_chain(int dirs) {
   if (dirs == 1) return reinterpret_cast<const void*>(&k_scan_bwd_chain<IO, 1, DYC>);
-  if (dirs == 2) return reinterpret_cast<const void*>(&k_scan_bwd_chain<IO, 2, DYC>);
-  return reinterpret_cast<const void*>(&k_scan_bwd_chain<IO, 3, DYC>);
+  return reinterpret_cast<const void*>(&k_scan_bwd_chain<IO, 2, DYC>);
 }
 
 template <class IO>
@@ -478,23 +477,23 @@ const void* pick_bwd_chain(int dirs, bool dyc) {
   return dyc ? pick_bwd_chain<IO, true>(dirs) : pick_bwd_chain<IO, false>(dirs);
 }
 
-// Chunks per row when the geometry can take the chained walk: one branch,
-// rows a multiple of the chunk size, a mean segment of 1 to kChainMaxMean
-// chunks (32 for the backward), one workgroup per chunk within the grid
-// limit; 0 otherwise.  Measured on MI355X against the per-item walks (C =
+// Chunks per row when the geometry can take the chained walk: rows a
+// multiple of the chunk size, a mean segment of 1 to kChainMaxMean chunks
+// (32 for the backward), one workgroup per chunk within the grid limit; 0
+// otherwise.  Measured on MI355X against the per-item walks (C =
 // 1536, uniform segments), fp32 forward / backward TB/s:
 //   8K elements 5.9 / 5.8 against 5.8 / 5.5;  32K 6.1 / 5.9 against 5.7 / 5.6;
 //   64K 6.2 / 6.3 against 5.9 / 5.5;  128K 5.5 / 5.9 against 5.9 / 5.5;
-//   512K 4.4 / 5.1 against 5.8 / 5.5 (a wave composes up to 63 slots per
-//   poll and the 64-chunk checkpoints serialise);
-// bf16 alike (64K: 5.4 / 5.6 against 5.0 / 4.9).  The two-branch launch
-// measured slower than the per-item walks (16K segments: 5.7 / 5.7 against
-// 6.1 / 6.0), so it keeps them.
+//   512K 4.4 / 5.1 against 5.8 / 5.5 (a chunk waits for every aggregate of
+//   its window, so long windows suffer from stragglers; checkpoints every 8
+//   or 16 chunks serialise instead and were slower still);
+// bf16 alike (64K: 5.4 / 5.6 against 5.0 / 4.9).  Two-branch calls launch
+// each branch on its own: both in one grid ran at 5.8 / 5.8 (cfg4) where
+// one branch at a time runs 6.2 / 6.0 (the per-item walks: 6.1 / 5.8).
 constexpr int64_t kChainMaxMeanFwd = 16, kChainMaxMeanBwd = 32;
 int64_t chain_rows(int64_t S, int64_t C, int64_t T, int v, int nbranch,
                    bool bwd) {
   const int64_t CH = chain_elems(v);
-  if (nbranch != 1) return 0;
   if (S <= 0 || C <= 0 || T <= 0 || T % CH != 0) return 0;
   const int64_t mean = T / S;
   if (mean < CH || mean > (bwd ? kChainMaxMeanBwd : kChainMaxMeanFwd) * CH)
@@ -536,8 +535,8 @@ int chain_setup(const ChainGeo& q, int v, void* ws, void* stream) {
   return e == hipSuccess ? ASC_OK : static_cast<int>(e);
 }
 
-int64_t chain_need(int64_t C, int64_t kr) {
-  return kChainFlagBytes + C * kr * static_cast<int64_t>(sizeof(LbSlot));
+int64_t chain_need(int64_t C, int64_t kr, int nbranch) {
+  return kChainFlagBytes + nbranch * C * kr * static_cast<int64_t>(sizeof(LbSlot));
 }
 
 // Common conditions: a workspace, all tensors 16-byte aligned (phase 0), a
@@ -547,7 +546,7 @@ bool chain_ready(const Geometry& g, bool aln, int v, void* ws,
   if (!ws || reinterpret_cast<uintptr_t>(ws) % 32 != 0) return false;
   if (!aln || g.phase != 0) return false;
   const int64_t kr = chain_rows(g.S, g.C, g.T, v, g.nbranch, bwd);
-  return kr > 0 && ws_bytes >= chain_need(g.C, kr);
+  return kr > 0 && ws_bytes >= chain_need(g.C, kr, g.nbranch);
 }
 
 }  // namespace
@@ -557,7 +556,7 @@ int64_t chain_bytes(int64_t S, int64_t C, int64_t T, int v, int nbranch) {
   // both calls)
   int64_t kr = chain_rows(S, C, T, v, nbranch, true);
   if (kr == 0) kr = chain_rows(S, C, T, v, nbranch, false);
-  return kr == 0 ? 0 : chain_need(C, kr);
+  return kr == 0 ? 0 : chain_need(C, kr, nbranch);
 }
 
 bool chain_fwd(const FwdParams& p, int dtype, bool aln, int dirs, void* ws,
@@ -570,13 +569,22 @@ bool chain_fwd(const FwdParams& p, int dtype, bool aln, int dirs, void* ws,
   for (int b = 0; b < p.geo.nbranch; ++b) q.br[b] = p.br[b];
   q.slots = reinterpret_cast<LbSlot*>(static_cast<char*>(ws) + kChainFlagBytes);
   if ((status = chain_setup(q.geo, v, ws, stream))) return true;
-  const void* fn = nullptr;
-  switch (dtype) {
-    case ASC_F32: fn = pick_fwd_chain<IoF32>(dirs); break;
-    case ASC_F16: fn = pick_fwd_chain<IoF16>(dirs); break;
-    default: fn = pick_fwd_chain<IoBF16>(dirs); break;
-  }
-  status = launch(fn, q.geo.nchunks * q.geo.nbranch, kChainWaves, q, stream);
+  // one launch per branch (both branches in one grid measured slower)
+  auto one = [&](int b, int d) {
+    ChainFwdParams r = q;
+    r.geo.nbranch = 1;
+    r.br[0] = p.br[b];
+    r.slots = q.slots + b * q.geo.nchunks;
+    const void* fn = nullptr;
+    switch (dtype) {
+      case ASC_F32: fn = pick_fwd_chain<IoF32>(d); break;
+      case ASC_F16: fn = pick_fwd_chain<IoF16>(d); break;
+      default: fn = pick_fwd_chain<IoBF16>(d); break;
+    }
+    return launch(fn, r.geo.nchunks, kChainWaves, r, stream);
+  };
+  status = dirs == 3 ? one(0, 1) : one(0, dirs);
+  if (status == ASC_OK && dirs == 3) status = one(1, 2);
   *skip = static_cast<const uint32_t*>(ws);
   return true;
 }
@@ -594,13 +602,22 @@ bool chain_bwd(const BwdParams& p, int dtype, bool aln, bool dyc, int dirs,
   }
   q.slots = reinterpret_cast<LbSlot*>(static_cast<char*>(ws) + kChainFlagBytes);
   if ((status = chain_setup(q.geo, v, ws, stream))) return true;
-  const void* fn = nullptr;
-  switch (dtype) {
-    case ASC_F32: fn = pick_bwd_chain<IoF32>(dirs, dyc); break;
-    case ASC_F16: fn = pick_bwd_chain<IoF16>(dirs, dyc); break;
-    default: fn = pick_bwd_chain<IoBF16>(dirs, dyc); break;
-  }
-  status = launch(fn, q.geo.nchunks * q.geo.nbranch, kChainWaves, q, stream);
+  auto one = [&](int b, int d) {
+    ChainBwdParams r = q;
+    r.geo.nbranch = 1;
+    r.br[0] = p.br[b];
+    r.dy_rs[0] = p.dy_rs[b];
+    r.slots = q.slots + b * q.geo.nchunks;
+    const void* fn = nullptr;
+    switch (dtype) {
+      case ASC_F32: fn = pick_bwd_chain<IoF32>(d, dyc); break;
+      case ASC_F16: fn = pick_bwd_chain<IoF16>(d, dyc); break;
+      default: fn = pick_bwd_chain<IoBF16>(d, dyc); break;
+    }
+    return launch(fn, r.geo.nchunks, kChainWaves, r, stream);
+  };
+  status = dirs == 3 ? one(0, 1) : one(0, dirs);
+  if (status == ASC_OK && dirs == 3) status = one(1, 2);
   *skip = static_cast<const uint32_t*>(ws);
   return true;
 }

@@ -86,7 +86,7 @@ def test_workspace_bytes():
   # 256-byte flag plus one 16-byte slot per chunk and branch; other
   # geometries run the workspace-free walks and need none
   assert lib.asc_scan_workspace_bytes(8, 1536, 524288, 0, 1) == 256 + 16 * 1536 * 128
-  assert lib.asc_scan_workspace_bytes(8, 1536, 131072, 0, 2) == 0   # two branches
+  assert lib.asc_scan_workspace_bytes(8, 1536, 131072, 0, 2) == 256 + 16 * 2 * 1536 * 32
   assert lib.asc_scan_workspace_bytes(1, 1536, 524288, 0, 1) == 0     # 128 chunks
   assert lib.asc_scan_workspace_bytes(8, 1536, 524288, 2, 1) == 256 + 16 * 1536 * 64
   assert lib.asc_scan_workspace_bytes(8, 1536, 524289, 0, 1) == 0     # ragged rows

@@ -901,17 +901,17 @@ def test_chain_walk_bounded_wait_fallback():
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16],
                          ids=["f32", "bf16"])
-def test_bidirectional_aligned_long_segments(dtype):
-  """Both branches with chunk-aligned long segments over 130 rows: the
-  two-branch launches keep the per-item walks (no workspace is asked for)."""
+def test_chain_walk_bidirectional(dtype):
+  """Both branches with chunk-aligned long segments over 130 rows (one
+  chained launch per branch)."""
   from associative_scan_triton import _lib, _ops
   CH = _chunk(dtype)
   lens, C = [CH, 2 * CH], 130
   gf, xf, dyf = make(lens, C, dtype, seed=1, glo=0.5, n=3)
   gb, xb, dyb = make(lens, C, dtype, seed=2, glo=0.5, n=3)
   T = sum(lens)
-  assert _lib.load().asc_scan_workspace_bytes(len(lens), C, T,
-                                              _lib.dtype_code(gf), 2) == 0
+  assert _lib.load().asc_scan_workspace_walk(len(lens), C, T,
+                                             _lib.dtype_code(gf), 2) == _lib.WALK_CHAINED
   cu = torch.tensor(cu_of(lens), device=DEV)
   d = [t.to(DEV) for t in (gf, xf, gb, xb, dyf, dyb)]
   hf, hb = torch.empty_like(d[0]), torch.empty_like(d[0])
