@@ -671,11 +671,14 @@ __device__ inline bool skipped(const Params& p) {
 }
 
 // Grid of a per-item walk launched behind the chained walk (usually
-// skipped): at most 32768 waves (128 per CU, more than fit at once), the
-// grid-stride loops take the rest, so that the skip costs a bounded number
-// of workgroups, not one per item (measured: 12 us for 12288 16-wave
-// workgroups; the 16-wave walk with 2048 workgroups ran cfg5 within 0.3%).
-constexpr int64_t kSkippableWaves = 32768;
+// skipped): at most 131072 waves (512 per CU), the grid-stride loops take
+// the rest, so that the skip costs a bounded number of workgroups, not one
+// per item.  A tighter cap hands each workgroup several ragged items when
+// the walk does run (varlen, 32 segments of 1000-15000 fp32 elements x 1024
+// rows, 8-wave walk: 32768 waves 807 / 1201 us fwd / bwd, 131072 waves
+// 726 / 1048, uncapped 721 / 1011); a looser one costs more when skipped
+// (bidirectional 8 x 16K x 1536: uncapped 683 us bwd against 673-675).
+constexpr int64_t kSkippableWaves = 131072;
 template <class Params>
 inline int64_t walk_grid(const Params& p, int64_t blocks, int waves_per_block) {
   const int64_t cap = kSkippableWaves / waves_per_block;
