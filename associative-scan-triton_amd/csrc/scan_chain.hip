@@ -35,6 +35,11 @@
 namespace asc {
 namespace {
 
+// Chunk shape, measured on MI355X (fp32, C = 1536, 64K / 16K segments,
+// forward / backward TB/s): 8 waves x 2 sub-tiles 6.18 / 6.26 and 6.09 /
+// 5.97; 8 x 4 6.05 / 6.00 and 5.74 / 5.53; 16 x 2 5.96 / 6.09 and 5.68 /
+// 5.56; 16 x 4 5.72 / 5.58; 4 x 2 5.06 / 5.64 (64K); one sub-tile per
+// wave (8 or 16 waves) 4.2-5.2 forward.
 constexpr int kChainWaves = 8;  // waves per workgroup (one chunk)
 constexpr int kChainU = 2;      // sub-tiles per wave
 constexpr int64_t kChainFlagBytes = 256;  // workspace: flag word, then slots
