@@ -17,6 +17,9 @@ row sample of the same inputs); and a parity check of sampled rows against
 the oracle, outside the timed region.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg5]
+
+--config sweep runs the reference's kernel benchmark sweep over T instead
+(see sweep()).
 """
 
 from __future__ import annotations
@@ -64,7 +67,8 @@ def parse():
   p.add_argument("--gpus", type=int, default=1)
   p.add_argument("--steps", type=int, default=20)
   p.add_argument("--warmup", type=int, default=5)
-  p.add_argument("--config", default="cfg5", choices=sorted(CONFIGS))
+  p.add_argument("--config", default="cfg5",
+                 choices=sorted(CONFIGS) + ["sweep"])
   p.add_argument("--no-cpu-baseline", action="store_true")
   p.add_argument("--no-check", action="store_true")
   p.add_argument("--no-api", action="store_true",
@@ -79,9 +83,12 @@ def main():
   a = parse()
   if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
     print(json.dumps({"error": "this build measures one GPU only; the scan "
-                      "shards over channels/sequences with no communication "
-                      "(see DESIGN.md); run with --gpus 1"}))
+                      "shards over channels/sequences with no communication, "
+                      "so one GPU's share at its real shape is the measured "
+                      "unit; run with --gpus 1"}))
     sys.exit(2)
+  if a.config == "sweep":
+    return sweep(a)
 
   import numpy as np
   import torch
@@ -348,6 +355,95 @@ def main():
     "api": api,
     "check": check,
   }
+  print(json.dumps(out), flush=True)
+
+
+# The reference's published kernel-level sweep (H100 80GB, README.md:142-187):
+# T -> (fwd+bwd, fwd, bwd) ms at B=8, C=1536, fp32, gates and tokens ~ U(0,1).
+H100_SWEEP = {
+  128: (0.027, 0.014, 0.020), 256: (0.043, 0.020, 0.029),
+  512: (0.077, 0.033, 0.049), 1024: (0.161, 0.068, 0.099),
+  2048: (0.306, 0.126, 0.186), 4096: (0.602, 0.240, 0.366),
+  8192: (1.186, 0.455, 0.722), 16384: (2.322, 0.926, 1.429),
+  32768: (4.602, 1.811, 2.821), 65536: (9.212, 3.606, 5.623),
+}
+
+
+def sweep(a):
+  """The reference's kernel benchmark sweep (bench/bench_kernels.py:279-312):
+  for each T, B=8 sequences of T packed along time, C=1536, fp32, gates and
+  tokens ~ U(0,1), dy = rand_like; the subjects forward, backward and
+  forward + backward are timed separately.  As the reference's
+  triton.testing.do_bench does, caches are flushed before every repetition
+  (here a 1 GiB write, four times the 256 MB MALL) and only the subject sits
+  between the two events; the median of the repetitions is reported."""
+  import numpy as np
+  import torch
+
+  from associative_scan_triton import _ops
+
+  dev = torch.device("cuda:0")
+  stream = torch.cuda.current_stream(dev)
+  B, C = 8, 1536
+  flush = torch.empty(1 << 28, dtype=torch.int32, device=dev)
+  reps = max(5, a.steps)
+  rows = []
+  for T in sorted(H100_SWEEP):
+    Tt = B * T
+    N = C * Tt
+    gen = torch.Generator(device=dev).manual_seed(1155)
+    cu = (torch.arange(B + 1, dtype=torch.int32) * T).to(dev)
+    g = torch.rand(C, Tt, device=dev, generator=gen)
+    x = torch.rand(C, Tt, device=dev, generator=gen)
+    dy = torch.rand(C, Tt, device=dev, generator=gen)
+    h, dx, dg = (torch.empty_like(x) for _ in range(3))
+
+    def fwd():
+      _ops.scan_fwd(g, x, h, cu, reverse=False)
+
+    def bwd():
+      _ops.scan_bwd(dy, g, h, dx, dg, cu, causal=True)
+
+    def both():
+      fwd()
+      bwd()
+
+    res = {}
+    for name, fn in (("fwd", fwd), ("bwd", bwd), ("fwd+bwd", both)):
+      for _ in range(a.warmup):
+        fn()
+      ts = []
+      for _ in range(reps):
+        flush.fill_(0)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1))
+      res[name] = float(np.median(ts))
+    ref = H100_SWEEP[T]
+    nbytes = 32 * N
+    row = {"T": T, "elements_per_tensor": N,
+           "fwd_ms": round(res["fwd"], 4), "bwd_ms": round(res["bwd"], 4),
+           "fwd_bwd_ms": round(res["fwd+bwd"], 4),
+           "fwd_bwd_GBs": round(nbytes / (res["fwd+bwd"] * 1e-3) / 1e9, 1),
+           "pct_peak": round(100 * nbytes / (res["fwd+bwd"] * 1e-3) / 1e9
+                             / PEAK_HBM_GBS, 1),
+           "h100_fwd_bwd_ms": ref[0],
+           "speedup_vs_h100": round(ref[0] / res["fwd+bwd"], 2)}
+    rows.append(row)
+    log(f"[sweep] {row}")
+    del g, x, dy, h, dx, dg
+    torch.cuda.empty_cache()
+  out = {"metric": "kernel-level fwd / bwd / fwd+bwd ms per T (median, "
+                   "caches flushed), B=8 C=1536 fp32",
+         "unit": "ms", "n_gpus": 1, "higher_is_better": False,
+         "dtype": "f32", "data": "synthetic (seeded device RNG, U(0,1))",
+         "config": {"workload": "sweep: the reference's kernel benchmark "
+                                "sweep over T, B=8 C=1536 fp32"},
+         "reps": reps, "warmup": a.warmup, "rows": rows}
   print(json.dumps(out), flush=True)
 
 
