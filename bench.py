@@ -367,6 +367,12 @@ H100_SWEEP = {
   8192: (1.186, 0.455, 0.722), 16384: (2.322, 0.926, 1.429),
   32768: (4.602, 1.811, 2.821), 65536: (9.212, 3.606, 5.623),
 }
+# and its API-level fwd+bwd (H100 80GB, README.md:97-108): T -> ms for
+# bench_vs_warpscan.py:214-220's subject (clone both inputs, scan_causal,
+# out.sum().backward()).
+H100_API = {128: 0.143, 256: 0.136, 512: 0.152, 1024: 0.300, 2048: 0.555,
+            4096: 1.069, 8192: 2.070, 16384: 4.087, 32768: 8.126,
+            65536: 16.238}
 
 
 def sweep(a):
@@ -376,10 +382,14 @@ def sweep(a):
   forward + backward are timed separately.  As the reference's
   triton.testing.do_bench does, caches are flushed before every repetition
   (here a 1 GiB write, four times the 256 MB MALL) and only the subject sits
-  between the two events; the median of the repetitions is reported."""
+  between the two events; the median of the repetitions is reported.  The
+  API leg times the reference's API subject (bench_vs_warpscan.py:214-220):
+  clone gates and tokens with requires_grad, scan_causal, out.sum() and
+  backward, chunk_size min(next_pow2(T), 512)."""
   import numpy as np
   import torch
 
+  import associative_scan_triton as ast
   from associative_scan_triton import _ops
 
   dev = torch.device("cuda:0")
@@ -408,8 +418,18 @@ def sweep(a):
       fwd()
       bwd()
 
+    chunk = min(ast.next_power_of_2(T), 512)
+    args = {"cu_seqlens": cu, "chunk_size": chunk,
+            "grid": ast.get_grid(B + 1, T, chunk, C)}
+
+    def api():
+      gc = g.clone().requires_grad_(True)
+      xc = x.clone().requires_grad_(True)
+      ast.scan_causal(gc, xc, args).sum().backward()
+
     res = {}
-    for name, fn in (("fwd", fwd), ("bwd", bwd), ("fwd+bwd", both)):
+    for name, fn in (("fwd", fwd), ("bwd", bwd), ("fwd+bwd", both),
+                     ("api", api)):
       for _ in range(a.warmup):
         fn()
       ts = []
@@ -432,13 +452,16 @@ def sweep(a):
            "pct_peak": round(100 * nbytes / (res["fwd+bwd"] * 1e-3) / 1e9
                              / PEAK_HBM_GBS, 1),
            "h100_fwd_bwd_ms": ref[0],
-           "speedup_vs_h100": round(ref[0] / res["fwd+bwd"], 2)}
+           "speedup_vs_h100": round(ref[0] / res["fwd+bwd"], 2),
+           "api_fwd_bwd_ms": round(res["api"], 4),
+           "h100_api_ms": H100_API[T],
+           "api_speedup_vs_h100": round(H100_API[T] / res["api"], 2)}
     rows.append(row)
     log(f"[sweep] {row}")
     del g, x, dy, h, dx, dg
     torch.cuda.empty_cache()
-  out = {"metric": "kernel-level fwd / bwd / fwd+bwd ms per T (median, "
-                   "caches flushed), B=8 C=1536 fp32",
+  out = {"metric": "kernel-level fwd / bwd / fwd+bwd and API-level fwd+bwd "
+                   "ms per T (median, caches flushed), B=8 C=1536 fp32",
          "unit": "ms", "n_gpus": 1, "higher_is_better": False,
          "dtype": "f32", "data": "synthetic (seeded device RNG, U(0,1))",
          "config": {"workload": "sweep: the reference's kernel benchmark "
