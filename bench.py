@@ -19,7 +19,7 @@ the oracle, outside the timed region.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg5]
 
 --config sweep runs the reference's kernel benchmark sweep over T instead
-(see sweep()).
+(see sweep()); --config accuracy its accuracy benchmark (see accuracy()).
 """
 
 from __future__ import annotations
@@ -68,7 +68,7 @@ def parse():
   p.add_argument("--steps", type=int, default=20)
   p.add_argument("--warmup", type=int, default=5)
   p.add_argument("--config", default="cfg5",
-                 choices=sorted(CONFIGS) + ["sweep"])
+                 choices=sorted(CONFIGS) + ["sweep", "accuracy"])
   p.add_argument("--no-cpu-baseline", action="store_true")
   p.add_argument("--no-check", action="store_true")
   p.add_argument("--no-api", action="store_true",
@@ -89,6 +89,8 @@ def main():
     sys.exit(2)
   if a.config == "sweep":
     return sweep(a)
+  if a.config == "accuracy":
+    return accuracy(a)
 
   import numpy as np
   import torch
@@ -467,6 +469,84 @@ def sweep(a):
          "config": {"workload": "sweep: the reference's kernel benchmark "
                                 "sweep over T, B=8 C=1536 fp32"},
          "reps": reps, "warmup": a.warmup, "rows": rows}
+  print(json.dumps(out), flush=True)
+
+
+# The reference's published forward RMSE against the sequential fp64 gold
+# (H100, C=4, seed 42; README.md:266-281).
+PUBLISHED_RMSE = {
+  "fp32": {128: 6.55e-08, 512: 6.46e-08, 2048: 6.62e-08, 8192: 6.69e-08},
+  "fp16": {128: 4.51e-04, 512: 4.89e-04, 2048: 2.58e-04, 8192: 2.58e-04},
+  "bf16": {128: 3.59e-03, 512: 3.68e-03, 2048: 2.07e-03, 8192: 2.06e-03},
+}
+
+
+def accuracy(a):
+  """The reference's accuracy benchmark (bench/bench_accuracy.py:31-37,
+  76-95, 129-160): C=4 channels, one sequence of T in 128 ... 8192, for
+  fp32 / fp16 / bf16 storage; torch.manual_seed(42) before each case, gates
+  ~ U(0,1) and tokens ~ N(0,1) drawn on the device in fp32 and cast; the
+  forward output against the sequential fp64 scan of the cast inputs:
+  max abs error, max relative error where |gold| > eps(dtype), mean abs
+  error and RMSE, beside the reference's published RMSE where it has one.
+  The fused backward's RMSE (dy ~ N(0,1), against the fp64 adjoint of the
+  same stored states) is reported too; the reference publishes none.  The
+  fp64 sequential scans are the test oracle, used here as the checker."""
+  import numpy as np
+  import torch
+
+  import associative_scan_triton as ast
+  from associative_scan_triton import _ops
+  from oracle import oracle
+
+  dev = torch.device("cuda:0")
+  C = 4
+  rows = []
+  for T in (128, 256, 512, 1024, 2048, 4096, 8192):
+    for dt, name in ((torch.float32, "fp32"), (torch.float16, "fp16"),
+                     (torch.bfloat16, "bf16")):
+      torch.manual_seed(42)
+      g32 = torch.rand(C, T, device=dev)
+      x32 = torch.randn(C, T, device=dev)
+      g, x = g32.to(dt).contiguous(), x32.to(dt).contiguous()
+      cu = torch.tensor([0, T], device=dev, dtype=torch.int32)
+      cs = min(ast.next_power_of_2(T), 512)
+      out = torch.empty_like(x)
+      ast.forward_scan_full(g, x, cu, ast.get_grid(2, T, cs, C),
+                            REVERSE=False, CHUNK_SIZE=cs, TESTING=False,
+                            tokens_out=out)
+      dy = torch.randn(C, T, device=dev).to(dt)
+      dx, dg = torch.empty_like(x), torch.empty_like(x)
+      _ops.scan_bwd(dy, g, out, dx, dg, cu, causal=True)
+      torch.cuda.synchronize()
+      f64 = lambda t: t.detach().cpu().double().numpy()
+      cu_np = np.array([0, T], dtype=np.int64)
+      gold = oracle.scan_fwd(f64(g), f64(x), cu_np, False)
+      diff = np.abs(f64(out) - gold)
+      eps = float(torch.finfo(dt).eps)
+      safe = np.abs(gold) > eps
+      dx_ref, dg_ref = oracle.scan_bwd(f64(dy), f64(g), f64(out), cu_np, True)
+      pub = PUBLISHED_RMSE[name].get(T)
+      rmse = float(np.sqrt(np.mean(diff ** 2)))
+      row = {"T": T, "dtype": name,
+             "max_abs_err": float(diff.max()),
+             "max_rel_err": float((diff[safe] / np.abs(gold[safe])).max())
+             if safe.any() else 0.0,
+             "mean_abs_err": float(diff.mean()), "rmse": rmse,
+             "published_rmse": pub,
+             "rmse_over_published": round(rmse / pub, 3) if pub else None,
+             "bwd_rmse_dx": float(np.sqrt(np.mean((f64(dx) - dx_ref) ** 2))),
+             "bwd_rmse_dg": float(np.sqrt(np.mean((f64(dg) - dg_ref) ** 2))),
+             "finite": bool(torch.isfinite(out).all())}
+      rows.append(row)
+      log(f"[accuracy] {row}")
+  out = {"metric": "forward RMSE vs sequential fp64 gold, C=4, seed 42 "
+                   "(the reference's accuracy benchmark)",
+         "unit": "rmse", "n_gpus": 1, "higher_is_better": False,
+         "data": "synthetic (torch.manual_seed(42), device RNG)",
+         "config": {"workload": "accuracy: C=4, one sequence of T, "
+                                "fp32/fp16/bf16 storage, fp32 accumulation"},
+         "rows": rows}
   print(json.dumps(out), flush=True)
 
 
