@@ -45,6 +45,17 @@ constexpr int kChainU = 2;      // sub-tiles per wave
 constexpr int64_t kChainFlagBytes = 256;  // workspace: flag word, then slots
 constexpr int kChainBlock = 64;           // chunks per checkpoint
 
+// fp16/bf16 chunks keep their loaded vectors packed while the chunk waits
+// for its carry and unpack them again to apply it (fp32 unpacking is a
+// bitcast).  The empty asm marks the packed words as changed, so that the
+// compiler cannot reuse the first unpacking and keep 8 floats per vector
+// alive across the barrier instead of 4 words.
+template <class IO>
+__device__ inline void repack_point(uint4& q) {
+  if (IO::V != 4)
+    asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w));
+}
+
 constexpr int64_t chain_elems(int v) {
   return static_cast<int64_t>(kChainWaves) * kChainU * kWave * v;
 }
@@ -204,14 +215,14 @@ __device__ inline void chain_fwd_chunk(const ChainFwdParams& p, int br,
     const int64_t rr = b - k.row * p.geo.kr;
     k.e0 = k.row * p.geo.T + (REV ? p.geo.kr - 1 - rr : rr) * CH;
   }
-  float g[U][V], x[U][V];
+  uint4 gq[U], xq[U];
   int64_t vi[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int64_t i = static_cast<int64_t>(wv * U + u) * kWave + lane;
     vi[u] = REV ? (k.e0 + CH) / V - 1 - i : k.e0 / V + i;
-    IO::unpack(ld16(t.g + vi[u] * 16), g[u]);
-    IO::unpack(ld16(t.x + vi[u] * 16), x[u]);
+    gq[u] = ld16(t.g + vi[u] * 16);
+    xq[u] = ld16(t.x + vi[u] * 16);
   }
   if (!chain_chunk<CH>(p.geo, b, REV, k)) return;  // outside every segment
   const int64_t head = REV ? k.P1 - 1 : k.P0;
@@ -220,10 +231,13 @@ __device__ inline void chain_fwd_chunk(const ChainFwdParams& p, int br,
   float wa = 1.0f, wx = 0.0f;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
+    float g[V], x[V];
+    IO::unpack(gq[u], g);
+    IO::unpack(xq[u], x);
     if (u == 0 && hsub)
-      sc[u] = fwd_local<IO, REV, true>(g[u], x[u], vi[u] * V, head);
+      sc[u] = fwd_local<IO, REV, true>(g, x, vi[u] * V, head);
     else
-      sc[u] = fwd_local<IO, REV, false>(g[u], x[u], vi[u] * V, 0);
+      sc[u] = fwd_local<IO, REV, false>(g, x, vi[u] * V, 0);
     wx = fmaf(sc[u].ta, wx, sc[u].tx);
     wa = wa * sc[u].ta;
   }
@@ -254,11 +268,15 @@ __device__ inline void chain_fwd_chunk(const ChainFwdParams& p, int br,
   for (int w = 0; w < wv; ++w) c = fmaf(agg[w].x, c, agg[w].y);
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    float hf[V];
+    float g[V], x[V], hf[V];
+    repack_point<IO>(gq[u]);
+    repack_point<IO>(xq[u]);
+    IO::unpack(gq[u], g);
+    IO::unpack(xq[u], x);
     if (u == 0 && hsub)
-      fwd_apply<IO, REV, true>(g[u], x[u], vi[u] * V, head, sc[u], c, hf);
+      fwd_apply<IO, REV, true>(g, x, vi[u] * V, head, sc[u], c, hf);
     else
-      fwd_apply<IO, REV, false>(g[u], x[u], vi[u] * V, 0, sc[u], c, hf);
+      fwd_apply<IO, REV, false>(g, x, vi[u] * V, 0, sc[u], c, hf);
     st16(t.h + vi[u] * 16, IO::pack(hf));
     c = fmaf(sc[u].ta, c, sc[u].tx);
   }
@@ -329,26 +347,28 @@ __device__ inline void chain_bwd_chunk(const ChainBwdParams& p, int br,
     const int64_t rr = b - k.row * p.geo.kr;
     k.e0 = k.row * p.geo.T + (RB ? p.geo.kr - 1 - rr : rr) * CH;
   }
-  float y[U][V], g[U][V], h[U][V];
+  uint4 yq[U], gq[U], hq[U];
   int64_t vi[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int64_t i = static_cast<int64_t>(wv * U + u) * kWave + lane;
     vi[u] = RB ? (k.e0 + CH) / V - 1 - i : k.e0 / V + i;
-    if (!DYC) IO::unpack(ld16(t.dy + vi[u] * 16), y[u]);
-    IO::unpack(ld16(t.g + vi[u] * 16), g[u]);
-    IO::unpack(ld16(t.h + vi[u] * 16), h[u]);
+    yq[u] = DYC ? make_uint4(0, 0, 0, 0) : ld16(t.dy + vi[u] * 16);
+    gq[u] = ld16(t.g + vi[u] * 16);
+    hq[u] = ld16(t.h + vi[u] * 16);
   }
   // DYC: the gradient is the row's one value (every element of the chunk
   // lies in the segment)
   const float dyv =
       DYC ? IO::load1(t.dy + k.row * p.dy_rs[br] * IO::ES) : 0.0f;
-  if (DYC) {
+  auto unpack_y = [&](int u, float* y) {
+    if (DYC) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int e = 0; e < V; ++e) y[u][e] = dyv;
-  }
+      for (int e = 0; e < V; ++e) y[e] = dyv;
+    } else {
+      IO::unpack(yq[u], y);
+    }
+  };
   if (!chain_chunk<CH>(p.geo, b, RB, k)) return;
   const int64_t head = RB ? k.P1 - 1 : k.P0;  // B-order head and tail
   const int64_t tail = RB ? k.P0 : k.P1 - 1;
@@ -372,11 +392,14 @@ __device__ inline void chain_bwd_chunk(const ChainBwdParams& p, int br,
   float wa = 1.0f, wx = 0.0f, cg = gp;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
+    float g[V], y[V];
+    IO::unpack(gq[u], g);
+    unpack_y(u, y);
     if (masked(u))
-      sc[u] = bwd_local<IO, RB, true>(g[u], y[u], vi[u] * V, head, cg, gprv[u]);
+      sc[u] = bwd_local<IO, RB, true>(g, y, vi[u] * V, head, cg, gprv[u]);
     else
-      sc[u] = bwd_local<IO, RB, false>(g[u], y[u], vi[u] * V, 0, cg, gprv[u]);
-    cg = readlane(g[u][jl], kWave - 1);
+      sc[u] = bwd_local<IO, RB, false>(g, y, vi[u] * V, 0, cg, gprv[u]);
+    cg = readlane(g[jl], kWave - 1);
     wx = fmaf(sc[u].ta, wx, sc[u].tx);
     wa = wa * sc[u].ta;
   }
@@ -407,14 +430,25 @@ __device__ inline void chain_bwd_chunk(const ChainBwdParams& p, int br,
   for (int w = 0; w < wv; ++w) c = fmaf(agg[w].x, c, agg[w].y);
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const float hin = (u + 1 < U) ? readlane(h[u + 1][jf], 0) : hn;
+    float g[V], y[V], h[V], hnext[V];
+    repack_point<IO>(gq[u]);
+    repack_point<IO>(yq[u]);
+    repack_point<IO>(hq[u]);
+    IO::unpack(gq[u], g);
+    unpack_y(u, y);
+    IO::unpack(hq[u], h);
+    float hin = hn;
+    if (u + 1 < U) {
+      IO::unpack(hq[u + 1 < U ? u + 1 : u], hnext);
+      hin = readlane(hnext[jf], 0);
+    }
     float dx[V], dg[V];
     if (masked(u))
-      bwd_apply<IO, RB, true>(g[u], y[u], h[u], vi[u] * V, head, tail, gprv[u],
-                              hin, sc[u], c, dx, dg);
+      bwd_apply<IO, RB, true>(g, y, h, vi[u] * V, head, tail, gprv[u], hin,
+                              sc[u], c, dx, dg);
     else
-      bwd_apply<IO, RB, false>(g[u], y[u], h[u], vi[u] * V, 0, 0, gprv[u], hin,
-                               sc[u], c, dx, dg);
+      bwd_apply<IO, RB, false>(g, y, h, vi[u] * V, 0, 0, gprv[u], hin, sc[u],
+                               c, dx, dg);
     st16(t.dx + vi[u] * 16, IO::pack(dx));
     st16(t.dg + vi[u] * 16, IO::pack(dg));
     c = fmaf(sc[u].ta, c, sc[u].tx);
@@ -492,7 +526,8 @@ const void* pick_bwd_chain(int dirs, bool dyc) {
 //   512K 4.4 / 5.1 against 5.8 / 5.5 (a chunk waits for every aggregate of
 //   its window, so long windows suffer from stragglers; checkpoints every 8
 //   or 16 chunks serialise instead and were slower still);
-// bf16 alike (64K: 5.4 / 5.6 against 5.0 / 4.9).  Two-branch calls launch
+// bf16 5.9 / 5.7 at 64K against 5.0 / 4.9 (packed vectors held across the
+// barrier; 5.3 / 5.5 when they were held unpacked).  Two-branch calls launch
 // each branch on its own: both in one grid ran at 5.8 / 5.8 (cfg4) where
 // one branch at a time runs 6.2 / 6.0 (the per-item walks: 6.1 / 5.8).
 constexpr int64_t kChainMaxMeanFwd = 16, kChainMaxMeanBwd = 32;
