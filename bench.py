@@ -51,6 +51,10 @@ CONFIGS = {
   "cfg3": ("varlen causal fwd+bwd, 64 seqs U[16,8192], C=1024, bf16 storage, "
            "fp32 accumulate, g~U(0.5,1)", 64, 1024, None, "bfloat16", "causal",
            (0.5, 1.0)),
+  # not a BASELINE config: cfg5's shape with bf16 storage (fp32 accumulation)
+  "bf16": ("causal fwd+bwd, B=8 C=1536 T=65536, bf16 storage, fp32 "
+           "accumulate, g~0.99+0.01U(0,1)", 8, 1536, 65536, "bfloat16", "causal",
+           (0.99, 1.0)),
   # not a BASELINE config: the segment-aware shift of _shift_pad.py at cfg5's
   # tensor size (compiled semantics, pad at segment starts)
   "shift": ("shift_pad backward=True (compiled form), B=8 C=1536 T=65536, "
