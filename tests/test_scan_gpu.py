@@ -417,6 +417,102 @@ def test_reference_bidi_vs_gold(dtype, seqlen):
                              **REF_TOL[dtype])
 
 
+# The reference's causal sweep (test_scan_causal.py:75-130): one sequence,
+# chunk sizes 2..256, 1/2/32 channels, gates ~ U(0,1), tokens ~ N(0,1),
+# scan_causal then out.sum().backward().  The reference compares with JAX
+# (not installed here, rtol = atol = 1e-4); the oracle states the same
+# recurrences in fp64.
+CAUSAL_SWEEP = [(cs, nc, sl) for cs in [2 ** i for i in range(1, 9)]
+                for nc in (1, 2, 32) for sl in (1, 5, 32, 128)]
+
+
+@pytest.mark.parametrize("chunk_size,num_channels,seqlen", CAUSAL_SWEEP)
+def test_reference_causal_sweep(chunk_size, num_channels, seqlen):
+  gen = torch.Generator().manual_seed(1155)
+  g = torch.rand(num_channels, seqlen, generator=gen)
+  x = torch.randn(num_channels, seqlen, generator=gen)
+  gd, xd = g.to(DEV).requires_grad_(True), x.to(DEV).requires_grad_(True)
+  out = ast.scan_causal(gd, xd, grid_args([seqlen], num_channels, chunk_size))
+  out.sum().backward()
+  cu = cu_of([seqlen])
+  h = oracle.scan_fwd(npf(g), npf(x), cu, False)
+  dx, dg = oracle.scan_bwd(np.ones((num_channels, seqlen)), npf(g), h, cu, True)
+  for name, got, ref in (("forward", out, h), ("gate grad", gd.grad, dg),
+                         ("token grad", xd.grad, dx)):
+    check_close(got, ref, torch.float32, name)
+    assert torch.allclose(got.detach().cpu().double(), torch.from_numpy(ref),
+                          rtol=1e-4, atol=1e-4), name
+
+
+# test_scan_kernels.py:287-467: forward_scan_full with a grid of several
+# chunks per sequence against one chunk per sequence (10 sequences of
+# `seqlen`, in place with the gate product, both directions).  The reference
+# computes torch.allclose without asserting it; here every launch scans whole
+# segments, so the two must agree bit for bit, and they are also checked
+# against the oracle.
+@pytest.mark.parametrize("reverse", [False, True], ids=["causal", "reverse"])
+@pytest.mark.parametrize("seqlen,chunk_size,no_channels",
+                         [(4, 2, 2), (8, 4, 1), (8, 4, 2), (8, 4, 3), (8, 2, 1),
+                          (8, 2, 2), (8, 2, 3), (16, 8, 2), (16, 4, 2),
+                          (16, 2, 2)])
+def test_reference_one_vs_multiple_chunks(seqlen, chunk_size, no_channels,
+                                          reverse):
+  lens = [seqlen] * 10
+  gen = torch.Generator().manual_seed(1155)
+  g = torch.rand(no_channels, seqlen * 10, generator=gen)
+  x = torch.rand(no_channels, seqlen * 10, generator=gen)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  outs = []
+  for cs in (chunk_size, seqlen):
+    gd, xd = g.to(DEV), x.to(DEV)
+    grid = ast.get_grid(len(cu), seqlen, cs, no_channels)
+    ast.forward_scan_full(gates=gd, tokens=xd, cu_seqlens=cu, CHUNK_SIZE=cs,
+                          grid=grid, REVERSE=reverse)
+    outs.append((gd, xd))
+  assert torch.equal(outs[0][0], outs[1][0]), "gate products"
+  assert torch.equal(outs[0][1], outs[1][1]), "states"
+  h, a = oracle.scan_fwd(npf(g), npf(x), cu_of(lens), reverse, gate_prod=True)
+  check_close(outs[0][1], h, torch.float32, "states")
+  check_close(outs[0][0], a, torch.float32, "gate products")
+
+
+# The reference's bidirectional sweep (test_scan_bidi.py:21-128, and
+# :129-200 with testing=False where the chunk covers the sequence): one
+# sequence, chunk sizes 2..256 (below the sequence length too), 1/2/32
+# channels, loss = out_fwd.sum() + out_bwd.sum().  The reference compares with
+# JAX's lax.associative_scan (jax is not installed here); the oracle states
+# the same recurrences in fp64, and both the reference's own tolerance and
+# the fp32 bound of these tests are checked.
+BIDI_SWEEP = [(t, cs, nc, sl) for t in (True, False)
+              for cs in [2 ** i for i in range(1, 9)]
+              for nc in (1, 2, 32) for sl in (1, 5, 32, 128)
+              if t or cs >= sl]
+
+
+@pytest.mark.parametrize("testing,chunk_size,num_channels,seqlen", BIDI_SWEEP)
+def test_reference_bidi_sweep(testing, chunk_size, num_channels, seqlen):
+  gen = torch.Generator().manual_seed(1155)
+  ts = [torch.rand(num_channels, seqlen, generator=gen) for _ in range(4)]
+  leaves = [t.to(DEV).requires_grad_(True) for t in ts]
+  args = grid_args([seqlen], num_channels, chunk_size)
+  yf, yb = ast.scan_bidirectional_branched(*leaves, args, testing=testing)
+  (yf.sum() + yb.sum()).backward()
+  cu = cu_of([seqlen])
+  ones = np.ones((num_channels, seqlen))
+  hf = oracle.scan_fwd(npf(ts[0]), npf(ts[1]), cu, False)
+  hb = oracle.scan_fwd(npf(ts[2]), npf(ts[3]), cu, True)
+  dxf, dgf = oracle.scan_bwd(ones, npf(ts[0]), hf, cu, True)
+  dxb, dgb = oracle.scan_bwd(ones, npf(ts[2]), hb, cu, False)
+  for name, got, ref in (("states fwd", yf, hf), ("states bwd", yb, hb),
+                         ("gates grad fwd", leaves[0].grad, dgf),
+                         ("tokens grad fwd", leaves[1].grad, dxf),
+                         ("gates grad bwd", leaves[2].grad, dgb),
+                         ("tokens grad bwd", leaves[3].grad, dxb)):
+    check_close(got, ref, torch.float32, name)
+    assert torch.allclose(got.detach().cpu().double(), torch.from_numpy(ref),
+                          rtol=1e-4, atol=1e-7), name
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
 @pytest.mark.parametrize("seqlen", [64, 512, 1024])
 def test_reference_bidi_backward_finite(dtype, seqlen):
