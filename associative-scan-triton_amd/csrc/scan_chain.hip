@@ -282,8 +282,12 @@ __device__ inline void chain_fwd_chunk(const ChainFwdParams& p, int br,
   }
 }
 
+// fp16/bf16: asked for 8 waves per SIMD, the forward fits 55-62 VGPRs
+// without spilling (77-85 unasked, 5-6 waves): 8 x 64K segments bf16 5.90 ->
+// 6.05 TB/s, fp16 5.43 -> 6.1.  The backward spills 28-76 bytes per lane at
+// 8 waves and is slower so (bf16 5.55 against 5.7 TB/s), so it is not asked.
 template <class IO, int DIRS>
-__global__ void __launch_bounds__(kChainWaves* kWave)
+__global__ void __launch_bounds__(kChainWaves* kWave, IO::V == 4 ? 1 : 8)
     k_scan_fwd_chain(ChainFwdParams p) {
   __shared__ float2 agg[kChainWaves];
   __shared__ float carry_s;
