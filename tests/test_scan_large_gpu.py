@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import DEV, check_close, npf
+from _helpers import DEV, check_close, cu_of, make, npf, oracle_fwd
 from associative_scan_triton import _ops
 from oracle import oracle
 
@@ -293,3 +293,79 @@ def test_mixed_short_segments(dtype):
   check_close(d[1], dgf, dtype, "dg fwd branch")
   check_close(d[2], dxb, dtype, "dx bwd branch")
   check_close(d[3], dgb, dtype, "dg bwd branch")
+
+
+# ---------------------------------------------------------------------------
+# randomized geometries around the walk-selection thresholds
+# ---------------------------------------------------------------------------
+
+def _random_cases(n, seed=20251202):
+  """(dtype, lens, C) draws whose shapes straddle the host's walk choices:
+  at most 128 items (look-back), more than 128 items with rows a whole
+  number of chunks and aligned or unaligned edges (chained walk, or its
+  fallback), long segments with many items (workgroup walks), short ragged
+  segments (one wave per item), and fp16/bf16 with few long items (16-wave
+  workgroups without a workspace).  At most 4M elements per tensor."""
+  rng = np.random.default_rng(seed)
+  dts = [torch.float32, torch.float16, torch.bfloat16]
+  cases = []
+  for i in range(n):
+    kind = i % 6
+    dt = dts[(i // 6) % 3]  # every kind in every dtype
+    ch = 4096 if dt == torch.float32 else 8192
+    if kind == 0:    # few items
+      S, C = int(rng.integers(1, 5)), int(rng.integers(1, 33))
+      lens = rng.integers(1, 40000, S).tolist()
+    elif kind in (1, 2):  # chunk-multiple rows, > 128 items
+      S = int(rng.integers(2, 6))
+      lens = (rng.integers(1, 4, S) * ch).tolist()
+      C = 129 // S + 1 + int(rng.integers(0, 20))
+      if kind == 2:  # move one edge off the chunk grid
+        cut = int(rng.integers(1, ch))
+        lens[0] += cut
+        lens[1] -= cut
+    elif kind == 3:  # long segments, many items
+      S, C = 1, int(rng.integers(130, 200))
+      lens = rng.integers(8192, 20000, S).tolist()
+    elif kind == 4:  # short ragged segments
+      S, C = int(rng.integers(5, 40)), int(rng.integers(3, 60))
+      lens = rng.integers(0, 3000, S).tolist()
+    else:            # few long items (fp16/bf16 16-wave workgroups)
+      S, C = 1, int(rng.integers(2, 20))
+      lens = rng.integers(16 * 16 * 512, 16 * 16 * 512 + 5000, S).tolist()
+    if sum(lens) == 0:
+      lens[0] = 1
+    lens = [int(v) for v in lens]
+    assert min(lens) >= 0 and C * sum(lens) <= 4_000_000, (lens, C)
+    cases.append((dt, lens, int(C)))
+  return cases
+
+
+@pytest.mark.parametrize("case", list(enumerate(_random_cases(36))),
+                         ids=lambda c: f"r{c[0]}")
+def test_random_geometries(case):
+  """Forward (both directions) and backward (both) of every row against the
+  oracle, with the workspace (whatever walk the geometry takes) and without
+  it (the workspace-free walks)."""
+  from associative_scan_triton import _ops
+  _, (dtype, lens, C) = case
+  g, x, dy = make(lens, C, dtype, glo=0.5, n=3, seed=11 + sum(lens) % 97)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  gd, xd, dyd = g.to(DEV), x.to(DEV), dy.to(DEV)
+  prev = _ops.USE_WORKSPACE
+  try:
+    for use_ws in (True, False):
+      _ops.USE_WORKSPACE = use_ws
+      for rev in (False, True):
+        h = torch.empty_like(gd)
+        _ops.scan_fwd(gd, xd, h, cu, rev)
+        href = oracle_fwd(g, x, lens, reverse=rev)
+        check_close(h, href, dtype, f"h ws={use_ws} rev={rev} {lens} C={C}")
+        dx, dg = torch.empty_like(gd), torch.empty_like(gd)
+        _ops.scan_bwd(dyd, gd, h, dx, dg, cu, causal=not rev)
+        dxr, dgr = oracle.scan_bwd(npf(dy), npf(g), npf(h), cu_of(lens),
+                                   not rev)
+        check_close(dx, dxr, dtype, f"dx ws={use_ws} rev={rev} {lens} C={C}")
+        check_close(dg, dgr, dtype, f"dg ws={use_ws} rev={rev} {lens} C={C}")
+  finally:
+    _ops.USE_WORKSPACE = prev
