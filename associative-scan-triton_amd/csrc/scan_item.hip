@@ -10,17 +10,22 @@ namespace {
 // Pipeline depth (sub-tiles per block) of the long-item kernels.
 constexpr int kFwdUnroll = 4, kBwdUnroll = 2;
 
-// Short items: a mean segment of at most 3 (fp32) or 4 (fp16/bf16)
-// sub-tiles.  Their waves run the shallow-pipeline kernels, whose lower
+// Short items: a mean segment of at most 4 sub-tiles (fp32 backward: 3).  Their waves run the shallow-pipeline kernels, whose lower
 // register count admits more waves per SIMD (fp32 forward 93 -> 57 VGPRs,
 // bf16 backward 125 -> 96).  Measured on MI355X, uniform segments of
 // C=1024 rows: bf16 1024 elements 4.9 / 5.6 -> 6.2 / 6.2 TB/s (fwd / bwd),
 // 512 elements 3.4 / 4.3 -> 4.3 / 5.0; fp32 600 elements 5.7 / 5.3 ->
 // 6.2 / 5.5; longer segments keep the deep pipeline (bf16 4096 elements:
 // 6.3 / 6.1 against 6.0 / 5.9 shallow).
-bool short_items(const Geometry& geo, int v) {
+// fp32 forward: up to 4 sub-tiles.  The deep forward pipeline only starts
+// past 4 sub-tiles, and at 4 its registers cost occupancy for nothing (T =
+// 1024: 29.8 against 31.0 us; ragged segments of 16-2048 elements: 122 against
+// 128 us); the backward is slower shallow at 4 (ragged 500-1500: 246 against
+// 242 us) and keeps 3.
+bool short_items(const Geometry& geo, int v, bool bwd) {
   const int64_t mean = geo.T / (geo.S > 0 ? geo.S : 1);
-  return mean <= (v == 4 ? 3 : 4) * static_cast<int64_t>(kWave) * v;
+  const int64_t subtiles = v != 4 ? 4 : (bwd ? 3 : 4);
+  return mean <= subtiles * static_cast<int64_t>(kWave) * v;
 }
 
 }  // namespace
@@ -28,7 +33,7 @@ bool short_items(const Geometry& geo, int v) {
 int item_fwd(FwdParams p, int dtype, int dirs, bool aln, bool wa,
              void* stream) {
   const void* fn = nullptr;
-  if (short_items(p.geo, 16 / elem_size(dtype))) {
+  if (short_items(p.geo, 16 / elem_size(dtype), false)) {
     fn = item_fwd_short_kernel(dtype, dirs, aln, wa);
   } else {
     switch (dtype) {
@@ -44,7 +49,7 @@ int item_fwd(FwdParams p, int dtype, int dirs, bool aln, bool wa,
 int item_bwd(BwdParams p, int dtype, int dirs, bool aln, bool dyc,
              void* stream) {
   const void* fn = nullptr;
-  if (short_items(p.geo, 16 / elem_size(dtype))) {
+  if (short_items(p.geo, 16 / elem_size(dtype), true)) {
     fn = item_bwd_short_kernel(dtype, dirs, aln, dyc);
   } else {
     switch (dtype) {
