@@ -369,3 +369,53 @@ def test_random_geometries(case):
         check_close(dg, dgr, dtype, f"dg ws={use_ws} rev={rev} {lens} C={C}")
   finally:
     _ops.USE_WORKSPACE = prev
+
+
+# ---------------------------------------------------------------------------
+# more than 2^31 elements per tensor (element indices past int32)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype,ragged",
+                         [(torch.float32, False), (torch.bfloat16, False),
+                          (torch.bfloat16, True)],
+                         ids=["f32-aligned", "bf16-aligned", "bf16-ragged"])
+def test_beyond_2pow31_elements(dtype, ragged):
+  """C = 2049 rows of T = 2^20 (2^31 + 2^20 elements per tensor): the last
+  row lies past element 2^31.  Aligned segments (8 of 2^17) take the
+  chained walk, ragged ones (9 lengths, odd) the workspace-free walks.
+  Inputs are drawn on the device; rows 0 and C-1 are checked against the
+  oracle, forward and backward, both directions."""
+  from associative_scan_triton import _ops
+  C, T = 2049, 1 << 20
+  if ragged:
+    lens = [131071, 3, 200000, 1, 99999, 300000, 77777, 65536, 0]
+    lens[-1] = T - sum(lens)
+  else:
+    lens = [T // 8] * 8
+  assert sum(lens) == T and C * T > 2 ** 31
+  gen = torch.Generator(device=DEV).manual_seed(31)
+  g = torch.rand(C, T, device=DEV, generator=gen).mul_(0.5).add_(0.5).to(dtype)
+  x = torch.randn(C, T, device=DEV, generator=gen).to(dtype)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  rows = [0, C - 1]
+  prev = _ops.USE_WORKSPACE
+  _ops.USE_WORKSPACE = not ragged
+  try:
+    for rev in (False, True):
+      h = torch.empty_like(x)
+      _ops.scan_fwd(g, x, h, cu, rev)
+      gs, xs = g[rows].cpu(), x[rows].cpu()
+      href = oracle_fwd(gs, xs, lens, reverse=rev)
+      check_close(h[rows], href, dtype, f"h rev={rev}")
+      dy = torch.randn(C, T, device=DEV, generator=gen).to(dtype)
+      dx, dg = torch.empty_like(x), torch.empty_like(x)
+      _ops.scan_bwd(dy, g, h, dx, dg, cu, causal=not rev)
+      dxr, dgr = oracle.scan_bwd(npf(dy[rows]), npf(gs), npf(h[rows]),
+                                 cu_of(lens), not rev)
+      check_close(dx[rows], dxr, dtype, f"dx rev={rev}")
+      check_close(dg[rows], dgr, dtype, f"dg rev={rev}")
+      del h, dy, dx, dg
+  finally:
+    _ops.USE_WORKSPACE = prev
+    del g, x
+    torch.cuda.empty_cache()
