@@ -419,3 +419,54 @@ def test_beyond_2pow31_elements(dtype, ragged):
     _ops.USE_WORKSPACE = prev
     del g, x
     torch.cuda.empty_cache()
+
+
+def test_beyond_2pow31_elements_lookback():
+  """5 bf16 rows of 2^29 (2^31 + 2^29 elements, 15 items: the look-back
+  walk, whose in-row offsets are 32-bit).  Each row holds a long segment and
+  two short ones; the short segments of the last row lie past element 2^31
+  and are checked against the oracle; the long segments of the first and
+  last row against the workspace-free walk (one 16-wave workgroup per
+  item), forward and backward."""
+  from associative_scan_triton import _lib, _ops
+  dtype = torch.bfloat16
+  C, T = 5, 1 << 29
+  lens = [T - 4096, 4093, 3]
+  lib = _lib.load()
+  assert lib.asc_scan_workspace_walk(len(lens), C, T, _lib.dtype_code(
+    torch.empty(0, dtype=dtype)), 1) == _lib.WALK_LOOKBACK
+  gen = torch.Generator(device=DEV).manual_seed(29)
+  g = torch.rand(C, T, device=DEV, generator=gen).mul_(0.5).add_(0.5).to(dtype)
+  x = torch.randn(C, T, device=DEV, generator=gen).to(dtype)
+  dy = torch.randn(C, T, device=DEV, generator=gen).to(dtype)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  prev = _ops.USE_WORKSPACE
+  try:
+    out = {}
+    for use_ws in (True, False):
+      _ops.USE_WORKSPACE = use_ws
+      h = torch.empty_like(x)
+      _ops.scan_fwd(g, x, h, cu, False)
+      dx, dg = torch.empty_like(x), torch.empty_like(x)
+      _ops.scan_bwd(dy, g, h, dx, dg, cu, causal=True)
+      # keep only what is compared: rows 0 and C-1
+      out[use_ws] = [t[[0, C - 1]].float() for t in (h, dx, dg)]
+      del h, dx, dg
+  finally:
+    _ops.USE_WORKSPACE = prev
+  s0 = T - 4096  # the short segments: the last 4096 elements of each row
+  short = [4093, 3]
+  gs, xs, dys = (t[C - 1, s0:].cpu()[None] for t in (g, x, dy))
+  href = oracle_fwd(gs, xs, short)
+  hl = out[True][0][1:, s0:]
+  check_close(hl, href, dtype, "h (short segments past 2^31)")
+  dxr, dgr = oracle.scan_bwd(npf(dys), npf(gs), npf(hl), cu_of(short), True)
+  check_close(out[True][1][1:, s0:], dxr, dtype, "dx (short segments)")
+  check_close(out[True][2][1:, s0:], dgr, dtype, "dg (short segments)")
+  # long segments: the two walks agree to the bf16 output rounding
+  for name, a, b in zip(("h", "dx", "dg"), out[True], out[False]):
+    err = (a[:, :s0] - b[:, :s0]).abs()
+    bound = 1e-2 * (1.0 + b[:, :s0].abs())
+    assert bool((err <= bound).all()), f"{name}: look-back vs workspace-free"
+  del g, x, dy, out
+  torch.cuda.empty_cache()
