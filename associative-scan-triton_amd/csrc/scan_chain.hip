@@ -530,8 +530,8 @@ const void* pick_bwd_chain(int dirs, bool dyc) {
 //   512K 4.4 / 5.1 against 5.8 / 5.5 (a chunk waits for every aggregate of
 //   its window, so long windows suffer from stragglers; checkpoints every 8
 //   or 16 chunks serialise instead and were slower still);
-// bf16 5.9 / 5.7 at 64K against 5.0 / 4.9 (packed vectors held across the
-// barrier; 5.3 / 5.5 when they were held unpacked).  Two-branch calls launch
+// bf16 6.05 / 5.7 at 64K against 5.0 / 4.9 (packed vectors held across the
+// barrier and 8 forward waves per SIMD; 5.3 / 5.5 before).  Two-branch calls launch
 // each branch on its own: both in one grid ran at 5.8 / 5.8 (cfg4) where
 // one branch at a time runs 6.2 / 6.0 (the per-item walks: 6.1 / 5.8).
 constexpr int64_t kChainMaxMeanFwd = 16, kChainMaxMeanBwd = 32;
