@@ -13,16 +13,32 @@ import torch
 from associative_scan_triton import _lib
 
 # Problems with few (segment, channel) items run the library's look-back walk,
-# which needs a workspace; the library says how large (0 = none needed).
-# False forces the workspace-free walks (the two agree to fp32 rounding).
+# and long chunk-aligned segments its chained walk; both need a workspace,
+# and the library says how large (0 = none needed).  False forces the
+# workspace-free walks (the walks agree to fp32 rounding).
 USE_WORKSPACE = True
+
+
+def _walk(lib, S: int, C: int, T: int, dtype_code: int, nbranch: int) -> int:
+  """The walk a workspace would buy for this geometry (0: none is used).
+
+  The look-back walk's last bits can vary from run to run (which
+  predecessor a tile meets as inclusive depends on timing); under
+  torch.use_deterministic_algorithms(True) it is not used, and the
+  workspace-free walks, which are bitwise reproducible, run instead."""
+  if not USE_WORKSPACE:
+    return 0
+  walk = lib.asc_scan_workspace_walk(S, C, T, dtype_code, nbranch)
+  if walk == _lib.WALK_LOOKBACK and torch.are_deterministic_algorithms_enabled():
+    return 0
+  return max(walk, 0)
 
 
 def _workspace(lib, dev: torch.device, S: int, C: int, T: int,
                dtype_code: int, nbranch: int):
   """A workspace from torch's caching allocator when the geometry wants one
   (the library clears it on the launch stream), else (None, 0)."""
-  if not USE_WORKSPACE:
+  if not _walk(lib, S, C, T, dtype_code, nbranch):
     return None, 0
   nbytes = lib.asc_scan_workspace_bytes(S, C, T, dtype_code, nbranch)
   if nbytes <= 0:
@@ -101,7 +117,9 @@ def scan_fwd(gates: torch.Tensor, tokens: torch.Tensor, h_out: torch.Tensor,
   cu = cu.contiguous()
   S, C, T = _geometry(tokens, cu, num_channels)
   with _OnDevice(dev):
-    ws, nb = (None, 0) if gate_prod_out is not None else _workspace(lib, dev, S, C, T, dt, 1)
+    # the gate product and in-place calls run the workspace-free walks
+    plain = gate_prod_out is None and h_out.data_ptr() != tokens.data_ptr()
+    ws, nb = _workspace(lib, dev, S, C, T, dt, 1) if plain else (None, 0)
     _lib.check(lib.asc_scan_fwd(
       gates.data_ptr(), tokens.data_ptr(), h_out.data_ptr(),
       _lib.ptr(gate_prod_out), cu.data_ptr(), cuc, S, C, T, dt,
@@ -120,7 +138,9 @@ def scan_bwd(grad: torch.Tensor, gates: torch.Tensor, states: torch.Tensor,
   cu = cu.contiguous()
   S, C, T = _geometry(grad, cu, num_channels)
   with _OnDevice(dev):
-    ws, nb = _workspace(lib, dev, S, C, T, dt, 1)
+    # d_tokens in place of the gradient runs the workspace-free walks
+    plain = d_tokens.data_ptr() != grad.data_ptr()
+    ws, nb = _workspace(lib, dev, S, C, T, dt, 1) if plain else (None, 0)
     _lib.check(lib.asc_scan_bwd(
       grad.data_ptr(), gates.data_ptr(), states.data_ptr(),
       d_tokens.data_ptr(), d_gates.data_ptr(), cu.data_ptr(), cuc, S, C, T,
@@ -184,8 +204,7 @@ def scan_bwd_any(grad: torch.Tensor, gates: torch.Tensor, states: torch.Tensor,
     lib = _lib.load()
     cu_c = cu.contiguous()
     S, C, T = _geometry(states, cu_c, num_channels)
-    if not USE_WORKSPACE or lib.asc_scan_workspace_walk(
-        S, C, T, _lib.dtype_code(states), 1) != _lib.WALK_LOOKBACK:
+    if _walk(lib, S, C, T, _lib.dtype_code(states), 1) != _lib.WALK_LOOKBACK:
       scan_bwd_rowgrad(grad, rs, gates, states, d_tokens, d_gates, cu_c,
                        causal, num_channels)
       return
@@ -282,8 +301,7 @@ def scan_bidi_bwd_any(dyf: torch.Tensor | None, dyb: torch.Tensor | None,
     lib = _lib.load()
     cu_c = cu.contiguous()
     S, C, T = _geometry(hf, cu_c, num_channels)
-    if not USE_WORKSPACE or lib.asc_scan_workspace_walk(
-        S, C, T, _lib.dtype_code(hf), 2) != _lib.WALK_LOOKBACK:
+    if _walk(lib, S, C, T, _lib.dtype_code(hf), 2) != _lib.WALK_LOOKBACK:
       scan_bidi_bwd_rowgrad(zero if dyf is None else dyf, rsf,
                             zero if dyb is None else dyb, rsb, gf, gb, hf, hb,
                             dxf, dgf, dxb, dgb, cu_c, num_channels)

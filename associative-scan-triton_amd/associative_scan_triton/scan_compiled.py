@@ -85,7 +85,7 @@ def _scan_causal_setup_context(ctx, inputs, output) -> None:
 def _scan_causal_backward(ctx, grad):
   states, gates = ctx.saved_tensors
   if grad is None:
-    grad = torch.zeros_like(states)
+    grad = states.new_zeros(()).expand_as(states)
   d_gates, d_tokens = scan_causal_bwd_op(
     grad, gates, states, ctx.cu_seqlens,
     ctx.num_chunks, ctx.no_channels, ctx.chunk_size,
@@ -170,6 +170,9 @@ def _scan_bidi_setup_context(ctx, inputs, output) -> None:
    cu_seqlens, num_chunks, no_channels, chunk_size) = inputs
   out_fwd, out_bwd = output
   ctx.save_for_backward(out_fwd, out_bwd, gates_fwd, gates_bwd)
+  # an output that receives no gradient arrives as None (read below as one
+  # zero value per row), not as a materialised zeros tensor
+  ctx.set_materialize_grads(False)
   ctx.cu_seqlens = cu_seqlens
   ctx.num_chunks = num_chunks
   ctx.no_channels = no_channels

@@ -741,6 +741,54 @@ inline int check_ptrs(const void* const* ptrs, int n, int es) {
   return ASC_OK;
 }
 
+// How the byte ranges [p, p + np) and [q, q + nq) meet: 0 = disjoint (or
+// either is empty or NULL), 1 = the same range, 2 = a partial overlap.
+enum { kDisjoint = 0, kSame = 1, kPartial = 2 };
+inline int overlap(const void* p, int64_t np, const void* q, int64_t nq) {
+  if (!p || !q || np <= 0 || nq <= 0) return kDisjoint;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uintptr_t b = reinterpret_cast<uintptr_t>(q);
+  if (a + static_cast<uintptr_t>(np) <= b || b + static_cast<uintptr_t>(nq) <= a)
+    return kDisjoint;
+  return (a == b && np == nq) ? kSame : kPartial;
+}
+
+// An output tensor and the one input it may replace in place (nullptr:
+// none), for the aliasing rule of the scan entry points.
+struct OutArg {
+  const void* p;
+  int64_t bytes;
+  const void* may_equal;
+};
+struct InArg {
+  const void* p;
+  int64_t bytes;
+};
+
+// Aliasing rule: an output may coincide exactly with the one input it is
+// allowed to replace; any other overlap of an output with an input or with
+// another output is ASC_E_ARG.  *inplace tells whether some output does
+// replace its input.
+inline int check_alias(const OutArg* outs, int nout, const InArg* ins, int nin,
+                       bool* inplace) {
+  *inplace = false;
+  for (int i = 0; i < nout; ++i) {
+    for (int j = 0; j < nin; ++j) {
+      const int ov = overlap(outs[i].p, outs[i].bytes, ins[j].p, ins[j].bytes);
+      if (ov == kDisjoint) continue;
+      if (ov == kSame && outs[i].may_equal == ins[j].p) {
+        *inplace = true;
+        continue;
+      }
+      return ASC_E_ARG;
+    }
+    for (int j = i + 1; j < nout; ++j)
+      if (overlap(outs[i].p, outs[i].bytes, outs[j].p, outs[j].bytes) != kDisjoint)
+        return ASC_E_ARG;
+  }
+  return ASC_OK;
+}
+
 template <class Params>
 int launch(const void* fn, int64_t blocks, int waves_per_block, Params p,
            void* stream) {

@@ -68,6 +68,24 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
   }
   all[n++] = a;
   if ((st = check_ptrs(all, n, es))) return st;
+  // h may replace the tokens of its branch and the gate product the gates
+  // (the reference's INPLACE and TESTING writes, _kernels.py:74-81).  Such
+  // a call runs the per-item walks, which read every element before they
+  // overwrite it: the bounded-wait fallbacks of the chained and look-back
+  // walks re-read inputs of earlier chunks, which an in-place call may
+  // already have overwritten.
+  const int64_t nbytes = C * T * es;
+  OutArg outs[3];
+  InArg ins[4];
+  int no = 0, ni = 0;
+  for (int b = 0; b < nbranch; ++b) {
+    outs[no++] = OutArg{h[b], nbytes, x[b]};
+    ins[ni++] = InArg{g[b], nbytes};
+    ins[ni++] = InArg{x[b], nbytes};
+  }
+  if (a) outs[no++] = OutArg{a, nbytes, g[0]};
+  bool inplace = false;
+  if ((st = check_alias(outs, no, ins, ni, &inplace))) return st;
   if (S == 0 || C == 0 || T == 0) return ASC_OK;
   const int ph = common_phase(all, n, es, v);
   const bool aln = ph >= 0;
@@ -83,12 +101,13 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
     p.br[b].pend = p.geo.phase + C * T;
   }
   const bool wa = a != nullptr;
-  // the look-back walks do not write the gate product; they need the
-  // caller's workspace (else the per-item walks run)
-  if (!wa && lb_use(S, C, T, nbranch, v)) {
+  // the look-back walks do not write the gate product and are not used in
+  // place; they need the caller's workspace (else the per-item walks run)
+  const bool walks_ok = !wa && !inplace;
+  if (walks_ok && lb_use(S, C, T, nbranch, v)) {
     if (lb_fwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st)) return st;
-  } else if (!wa && chain_fwd(p, dtype, aln, dirs, ws, ws_bytes, stream, st,
-                              &p.skip)) {
+  } else if (walks_ok && chain_fwd(p, dtype, aln, dirs, ws, ws_bytes, stream,
+                                   st, &p.skip)) {
     // the per-item walk below runs only if cu_seqlens turns out unaligned
     if (st) return st;
   }
@@ -123,6 +142,25 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
   }
   if ((st = check_ptrs(all, n, es))) return st;
   if ((st = check_ptrs(dy, nbranch, es))) return st;
+  // d_tokens may replace the (dense) gradient of its branch, and such a call
+  // runs the per-item walks (see run_fwd); any other overlap of an output
+  // with an input or another output is an error: the shifted gates and
+  // states are read across sub-tile and wave edges after neighbouring
+  // elements' outputs may have been stored.
+  const int64_t nbytes = C * T * es;
+  OutArg outs[4];
+  InArg ins[6];
+  int no = 0, ni = 0;
+  for (int b = 0; b < nbranch; ++b) {
+    const int64_t dyb = dyc ? ((C > 0 ? C - 1 : 0) * dy_rs[b] + 1) * es : nbytes;
+    outs[no++] = OutArg{dx[b], nbytes, dyc ? nullptr : dy[b]};
+    outs[no++] = OutArg{dg[b], nbytes, nullptr};
+    ins[ni++] = InArg{dy[b], dyb};
+    ins[ni++] = InArg{g[b], nbytes};
+    ins[ni++] = InArg{h[b], nbytes};
+  }
+  bool inplace = false;
+  if ((st = check_alias(outs, no, ins, ni, &inplace))) return st;
   if (S == 0 || C == 0 || T == 0) return ASC_OK;
   // the per-row gradient of dyc is read by scalar loads: its alignment does
   // not enter the phase
@@ -143,10 +181,10 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
     p.br[b].pend = p.geo.phase + C * T;
   }
   for (int b = 0; b < nbranch; ++b) p.dy_rs[b] = dyc ? dy_rs[b] : 0;
-  if (!dyc && lb_use(S, C, T, nbranch, v)) {
+  if (!inplace && !dyc && lb_use(S, C, T, nbranch, v)) {
     if (lb_bwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st)) return st;
-  } else if (chain_bwd(p, dtype, aln, dyc, dirs, ws, ws_bytes, stream, st,
-                       &p.skip)) {
+  } else if (!inplace && chain_bwd(p, dtype, aln, dyc, dirs, ws, ws_bytes,
+                                   stream, st, &p.skip)) {
     // the per-item walk below runs only if cu_seqlens turns out unaligned
     if (st) return st;
   }

@@ -1,3 +1,5 @@
+#include <atomic>
+
 #include "asc_common.h"
 #include "lookback_slots.h"
 
@@ -933,9 +935,11 @@ __global__ void __launch_bounds__(256) k_fill_zero(u64* p, int64_t n) {
     p[i] = 0;
 }
 
-// Look-back walk: polls before a waiting wave computes a missing
-// predecessor itself (a test hook can lower it to exercise that path).
-uint32_t g_spin_limit = 1u << 14;
+// Look-back and chained walks: polls before a waiting wave computes a
+// missing predecessor itself (a test hook can lower it to exercise that
+// path).  Process-wide; read once per launch on the host, so an atomic with
+// relaxed order is enough for concurrent callers on several host threads.
+std::atomic<uint32_t> g_spin_limit{1u << 14};
 
 // Tiles of the look-back walk: kLbWaves parts each, from the start of the
 // phase frame (the vectors of every element type divide 1024).
@@ -969,7 +973,7 @@ bool lb_prepare(const Geometry& geo, int v, void* ws, int64_t ws_bytes,
                 LbGeo& lg, int64_t& need) {
   if (!ws || reinterpret_cast<uintptr_t>(ws) % 32 != 0) return false;
   lg = LbGeo{geo.cu, geo.cu64, geo.S, geo.C, geo.T, geo.C * geo.T, geo.phase,
-             0, 0, geo.nbranch, g_spin_limit};
+             0, 0, geo.nbranch, g_spin_limit.load(std::memory_order_relaxed)};
   lg.nvec = (lg.phase + lg.n + v - 1) / v;
   lg.ntiles = lb_ntiles(lg.n, lg.phase, v);
   need = lg.ntiles * geo.nbranch * static_cast<int64_t>(sizeof(LbSlot));
@@ -1020,12 +1024,10 @@ int64_t lb_bytes(int64_t n, int v, int nbranch) {
   return lb_ntiles(n, v - 1, v) * nbranch * static_cast<int64_t>(sizeof(LbSlot));
 }
 
-unsigned lb_spin_limit() { return g_spin_limit; }
+unsigned lb_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
 
 unsigned lb_set_spin_limit(unsigned polls) {
-  const unsigned prev = g_spin_limit;
-  g_spin_limit = polls;
-  return prev;
+  return g_spin_limit.exchange(polls, std::memory_order_relaxed);
 }
 
 bool lb_fwd(const FwdParams& p, int dtype, int dirs, bool aln, void* ws,

@@ -93,11 +93,12 @@ int asc_scan_workspace_walk(int64_t num_seq, int64_t num_channels,
                             int64_t seq_stride, int dtype, int nbranch);
 
 /*
- * Test hook, no reference counterpart: sets how many times a look-back wave
- * polls a preceding tile's slot before it computes that tile's carry map
- * from the tile's inputs itself (0 = always compute; the default keeps the
- * fallback for pathological scheduling only).  Returns the previous value.
- * Affects launches issued after the call.
+ * Test hook, no reference counterpart: sets how many times a look-back or
+ * chained-walk wave polls a preceding tile's slot before it computes that
+ * tile's carry map from the tile's inputs itself (0 = always compute; the
+ * default keeps the fallback for pathological scheduling only).  Returns
+ * the previous value.  Process-wide (an atomic: safe to call from any host
+ * thread); affects launches issued after the call.
  */
 unsigned asc_set_lookback_spin_limit(unsigned polls);
 
@@ -111,8 +112,12 @@ const char* asc_strerror(int status);
  * gate_prod_out (nullable): also writes the running gate product
  *   A[t] = prod g over [start..t] (reverse: over [t..end-1]).
  * In-place use is allowed: h_out may equal tokens and gate_prod_out may
- * equal gates (each element is read before it is overwritten).  With
- * gate_prod_out the workspace-free walk is used.
+ * equal gates (each element is read before it is overwritten).  Such a call,
+ * and any call with gate_prod_out, runs the workspace-free walks (the
+ * bounded-wait fallbacks of the look-back and chained walks re-read inputs
+ * of earlier tiles, which an in-place call may already have overwritten).
+ * Any other overlap between an output and an input, or between the two
+ * outputs, returns ASC_E_ARG.
  *
  * Replaces: _dispatcher.py:12-70 forward_scan_full, which launches
  *   _kernels.py:19-81  forward_scan_chunked (one chunk) or
@@ -134,6 +139,12 @@ int asc_scan_fwd(const void* gates, const void* tokens, void* h_out,
  *   causal = 0 (backward of reverse=1):
  *     dx[t] = dy[t] + g[t-1]*dx[t-1],  dx[start] = dy[start]
  *     dg[t] = h[t+1]*dx[t],            h[end] := 0
+ * d_tokens may equal grad (then the workspace-free walks run); any other
+ * overlap between an output and an input or the other output returns
+ * ASC_E_ARG (the shifted gates and states are read across the edges of
+ * other waves' elements, which may already have been stored).  The same
+ * rule holds for the bidirectional and row-gradient entry points below, per
+ * branch.
  *
  * Replaces: _dispatcher.py:73-117 backward_scan_fused_full, which launches
  *   _kernels.py:171-287 backward_scan_fused or

@@ -118,9 +118,9 @@ def test_error_is_raised_with_message():
 
 def test_rowgrad_validation_codes():
   lib = _lib.load()
-  args = dict(grad=8, rs=0, gates=8, states=8, dx=8, dg=8, cu=8, cu_dtype=0,
-              S=1, C=1, T=4, dtype=0, causal=1, ws=None, ws_bytes=0,
-              stream=None)
+  args = dict(grad=8, rs=0, gates=64, states=128, dx=192, dg=256, cu=8,
+              cu_dtype=0, S=1, C=1, T=4, dtype=0, causal=1, ws=None,
+              ws_bytes=0, stream=None)
 
   def call(**kw):
     a = dict(args)
@@ -137,7 +137,10 @@ def test_rowgrad_validation_codes():
 
 def test_bidi_rowgrad_validation_codes():
   lib = _lib.load()
-  base = [8, 0, 8, 0] + [8] * 9 + [0, 1, 1, 4, 0, None, 0, None]
+  # row gradients, then gates, states and the four outputs 64 bytes apart
+  # (fp32, C=1, T=4: 16 bytes per tensor), then cu_seqlens
+  base = ([8, 0, 8, 0] + [64 * (i + 1) for i in range(8)] + [8]
+          + [0, 1, 1, 4, 0, None, 0, None])
 
   def call(i=None, v=None):
     a = list(base)
@@ -153,3 +156,43 @@ def test_bidi_rowgrad_validation_codes():
   assert call(17, 9) == -2        # dtype
   assert call(2, 6) == -4         # fp32 gradient not 4-byte aligned
   assert call(14, 0) == 0         # num_seq = 0: nothing launched
+
+
+def test_aliasing_rule_codes():
+  """An output may replace only its own input (h the tokens, the gate
+  product the gates, d_tokens the dense gradient); any other overlap is
+  ASC_E_ARG.  fp32, C=1, T=4: 16 bytes per tensor; S=0, so an accepted
+  call launches nothing."""
+  lib = _lib.load()
+  ok = dict(S=0, gates=64, tokens=128, h_out=192)
+  assert _fwd(lib, **ok) == 0
+  assert _fwd(lib, **{**ok, "h_out": 128}) == 0          # h replaces tokens
+  assert _fwd(lib, **{**ok, "h_out": 64}) == -5          # h over the gates
+  assert _fwd(lib, **{**ok, "h_out": 136}) == -5         # partial overlap
+  assert _fwd(lib, **{**ok, "gate_prod_out": 64}) == 0   # TESTING in place
+  assert _fwd(lib, **{**ok, "h_out": 128, "gate_prod_out": 64}) == 0
+  assert _fwd(lib, **{**ok, "gate_prod_out": 192}) == -5  # both outputs
+  assert _fwd(lib, **{**ok, "gate_prod_out": 128}) == -5  # A over tokens
+  assert _fwd(lib, **{**ok, "h_out": 60}) == -5          # ends inside gates
+  assert _fwd(lib, **{**ok, "h_out": 48}) == 0           # ends where gates begin
+
+  def bwd(grad=64, gates=128, states=192, dx=256, dg=320):
+    return lib.asc_scan_bwd(grad, gates, states, dx, dg, 8, 0, 0, 1, 4, 0, 1,
+                            None, 0, None)
+
+  assert bwd() == 0
+  assert bwd(dx=64) == 0          # d_tokens replaces the gradient
+  assert bwd(dg=64) == -5         # d_gates over the gradient
+  assert bwd(dx=128) == -5        # over the gates
+  assert bwd(dg=192) == -5        # over the states
+  assert bwd(dx=320) == -5        # the two outputs
+  assert bwd(dx=200) == -5        # partial overlap with the states
+  # bidirectional: an output of one branch over an input of the other
+  base = [64 * (i + 1) for i in range(6)] + [8, 0, 0, 1, 4, 0, None, 0, None]
+  assert lib.asc_scan_bidi_fwd(*base) == 0
+  bad = list(base)
+  bad[4] = bad[3]                 # h_fwd over tokens_bwd
+  assert lib.asc_scan_bidi_fwd(*bad) == -5
+  inplace = list(base)
+  inplace[4], inplace[5] = inplace[1], inplace[3]   # each branch in place
+  assert lib.asc_scan_bidi_fwd(*inplace) == 0

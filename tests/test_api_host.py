@@ -122,3 +122,20 @@ def test_row_constant_stride_detection():
   flat = torch.empty(300)
   assert row_constant_stride(torch.ones(()).expand(300), flat) == 0
   assert row_constant_stride(torch.ones(300), flat) is None
+
+
+def test_deterministic_mode_avoids_lookback():
+  """Under torch.use_deterministic_algorithms(True) the look-back walk (its
+  last bits can vary from run to run) is not used; the chained walk, whose
+  carries are composed in a fixed order, still is."""
+  from associative_scan_triton import _lib, _ops
+  lib = _lib.load()
+  assert _ops._walk(lib, 2, 4, 1_000_000, 0, 1) == _lib.WALK_LOOKBACK
+  prev = torch.are_deterministic_algorithms_enabled()
+  torch.use_deterministic_algorithms(True)
+  try:
+    assert _ops._walk(lib, 2, 4, 1_000_000, 0, 1) == 0
+    assert _ops._walk(lib, 8, 1536, 524288, 0, 1) == _lib.WALK_CHAINED
+  finally:
+    torch.use_deterministic_algorithms(prev)
+  assert _ops._walk(lib, 2, 4, 1_000_000, 0, 1) == _lib.WALK_LOOKBACK

@@ -315,3 +315,33 @@ def test_planted_mistakes_are_caught():
   _, dx_ref, _ = _loop_grads(g2, x2, dy2)
   h2 = oracle.scan_fwd(g2, x2, [0, 6])
   assert not np.allclose(_bwd_wrong_gate_index(dy2, g2, h2, [0, 6])[0], dx_ref)
+
+
+# ---------------------------------------------------------------------------
+# the CPU baseline's function (fp32 storage, fp64 accumulation)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("threads", [1, 4])
+def test_fwd_bwd_f32io_is_the_oracle_rounded(threads):
+  """fwd_bwd_f32io accumulates in fp64 from the fp32-stored inputs and
+  rounds each output once, so h and dx are the fp64 oracle's values rounded
+  to fp32, bit for bit, and dg is the oracle's dg of the stored fp32 states
+  rounded; checked against both restatements (C and numpy) on varlen
+  packing with an empty segment, for any thread count."""
+  rng = np.random.default_rng(7)
+  lens = [1, 37, 0, 300, 2, 1029]
+  cu = np.concatenate([[0], np.cumsum(lens)])
+  C, T = 6, int(cu[-1])
+  g = rng.uniform(0.5, 1.0, (C, T)).astype(np.float32)
+  x = rng.standard_normal((C, T)).astype(np.float32)
+  dy = rng.standard_normal((C, T)).astype(np.float32)
+  h, dx, dg = oracle.fwd_bwd_f32io(g, x, dy, cu, C, threads)
+  for fwd, bwd in ((oracle.scan_fwd, oracle.scan_bwd),
+                   (oracle.np_scan_fwd, oracle.np_scan_bwd)):
+    h64 = fwd(g, x, cu)
+    assert np.array_equal(h, h64.astype(np.float32))
+    dx64, dg64 = bwd(dy, g, h.astype(np.float64), cu)
+    assert np.array_equal(dx, dx64.astype(np.float32))
+    assert np.array_equal(dg, dg64.astype(np.float32))
+  # a dropped gate term in the backward would not go unnoticed
+  assert not np.array_equal(dx, dy)

@@ -27,8 +27,10 @@ def _rows(C):
 
 
 def _check_fwd_bwd(g, x, dy, h, dx, dg, cu, dtype, rows, reverse=False):
+  """dy None: the gradient of out.sum() (ones)."""
   cu_np = cu.cpu().numpy().astype(np.int64)
-  gs, xs, dys = npf(g[rows]), npf(x[rows]), npf(dy[rows])
+  gs, xs = npf(g[rows]), npf(x[rows])
+  dys = np.ones_like(gs) if dy is None else npf(dy[rows])
   h_ref = oracle.scan_fwd(gs, xs, cu_np, reverse)
   check_close(h[rows], h_ref, dtype, "h (sampled rows)")
   dx_ref, dg_ref = oracle.scan_bwd(dys, gs, npf(h[rows]), cu_np,
@@ -110,6 +112,52 @@ def test_cfg4_bidi_fp32_fwd_bwd():
   _check_fwd_bwd(gf, xf, dyf, hf, outs[0], outs[1], cu, torch.float32, rows)
   _check_fwd_bwd(gb, xb, dyb, hb, outs[2], outs[3], cu, torch.float32, rows,
                  reverse=True)
+
+
+def _api_args(cu, B, T, C):
+  import associative_scan_triton as ast
+  return {"cu_seqlens": cu, "chunk_size": 128,
+          "grid": ast.get_grid(B + 1, T, 128, C)}
+
+
+def test_cfg5_public_api_sum_backward():
+  """cfg5 through the public autograd API: scan_causal(...).sum().backward()
+  hands the backward a stride-0 gradient, which runs the chained walk's
+  row-gradient kernels over the whole 805M-element problem."""
+  import associative_scan_triton as ast
+  C, B, T = 1536, 8, 65536
+  gen = _gen(15)
+  g = torch.rand(C, B * T, device=DEV, generator=gen).mul_(0.01).add_(0.99)
+  x = torch.randn(C, B * T, device=DEV, generator=gen)
+  cu = torch.arange(B + 1, device=DEV, dtype=torch.int32) * T
+  gl, xl = g.requires_grad_(True), x.requires_grad_(True)
+  y = ast.scan_causal(gl, xl, _api_args(cu, B, T, C))
+  y.sum().backward()
+  torch.cuda.synchronize()
+  _check_fwd_bwd(g.detach(), x.detach(), None, y.detach(), xl.grad, gl.grad,
+                 cu, torch.float32, _rows(C))
+
+
+def test_cfg4_public_api_sum_backward():
+  """cfg4 through the public bidirectional API with both outputs summed:
+  both branches take the chained row-gradient kernels at full size."""
+  import associative_scan_triton as ast
+  C, B, T = 1536, 8, 16384
+  gen = _gen(14)
+  mk = lambda: torch.rand(C, B * T, device=DEV, generator=gen).mul_(0.1).add_(0.9)  # noqa: E731
+  gf, gb = mk(), mk()
+  xf = torch.randn(C, B * T, device=DEV, generator=gen)
+  xb = torch.randn(C, B * T, device=DEV, generator=gen)
+  cu = torch.arange(B + 1, device=DEV, dtype=torch.int32) * T
+  leaves = [t.requires_grad_(True) for t in (gf, xf, gb, xb)]
+  yf, yb = ast.scan_bidirectional_branched(*leaves, _api_args(cu, B, T, C))
+  (yf.sum() + yb.sum()).backward()
+  torch.cuda.synchronize()
+  rows = _rows(C)
+  _check_fwd_bwd(gf.detach(), xf.detach(), None, yf.detach(), xf.grad,
+                 gf.grad, cu, torch.float32, rows)
+  _check_fwd_bwd(gb.detach(), xb.detach(), None, yb.detach(), xb.grad,
+                 gb.grad, cu, torch.float32, rows, reverse=True)
 
 
 def test_cfg1_small_causal():
