@@ -17,7 +17,7 @@ from associative_scan_triton._build import LIB_PATH
 
 ASC_F32, ASC_F16, ASC_BF16 = 0, 1, 2
 ASC_CU_I32, ASC_CU_I64 = 0, 1
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _DTYPES = {
   torch.float32: ASC_F32,
@@ -40,6 +40,7 @@ SIGNATURES = {
   "asc_set_lookback_spin_limit": [_U],
   "asc_strerror": [_I],
   "asc_scan_fwd": [_P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P, _L, _P],
+  "asc_scan_fwd_noalloc": [_P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P],
   "asc_scan_bwd": [_P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P, _L, _P],
   "asc_scan_bwd_rowgrad": [_P, _L, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P, _L, _P],
   "asc_scan_bidi_fwd": [_P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _P, _L, _P],

@@ -6,7 +6,17 @@
 // shift_pad.hip: the shift entry point), over the shared sub-tile scan of
 // asc_common.h.
 
+#include <atomic>
+#include <mutex>
+
 #include "asc_common.h"
+
+// Workspace of the allocation-free forward (asc_scan_fwd_noalloc, below):
+// each GPU the library runs on holds its own copy until the process ends.
+// On the host this name is a host-side stand-in, not a device address; the
+// device address of the current GPU's copy comes from hipGetSymbolAddress.
+constexpr int64_t kScratchBytes = int64_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace asc {
 namespace {
@@ -193,6 +203,43 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
   return item_bwd(p, dtype, dirs, aln, dyc, stream);
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free forward (asc_scan_fwd_noalloc): the device address of the
+// current GPU's copy of `scratch` is looked up once per device and only
+// that address is ever handed to kernels.
+// ---------------------------------------------------------------------------
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's `scratch`; `stream` (if not NULL)
+// must belong to the current device.
+int scratch_ptr(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return ASC_E_ARG;
+  if (stream) {
+    int sdev = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (sdev != dev) return ASC_E_ARG;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return static_cast<int>(e);
+      if (!p) return ASC_E_NULL;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return ASC_OK;
+}
+
 }  // namespace
 }  // namespace asc
 
@@ -240,6 +287,9 @@ const char* asc_strerror(int status) {
     case ASC_E_SIZE: return "invalid (negative or overflowing) size argument";
     case ASC_E_ALIGN: return "pointer not aligned to its element size";
     case ASC_E_ARG: return "invalid argument";
+    case ASC_E_SCRATCH:
+      return "the geometry needs more workspace than the static scratch "
+             "buffer of asc_scan_fwd_noalloc holds (8 MiB)";
     default:
       if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
       return "unknown error";
@@ -257,6 +307,30 @@ int asc_scan_fwd(const void* gates, const void* tokens, void* h_out,
   return run_fwd(g, x, h, gate_prod_out, 1, reverse ? 2 : 1, cu_seqlens,
                  cu_dtype, num_seq, num_channels, seq_stride, dtype, workspace,
                  workspace_bytes, stream);
+}
+
+int asc_scan_fwd_noalloc(const void* gates, const void* tokens, void* h_out,
+                         void* gate_prod_out, const void* cu_seqlens,
+                         int cu_dtype, int64_t num_seq, int64_t num_channels,
+                         int64_t seq_stride, int dtype, int reverse,
+                         void* stream) {
+  // the workspace asc_scan_fwd would be given for this geometry, taken from
+  // the static array (the walks clear what must start at zero themselves)
+  const int64_t need = asc_scan_workspace_bytes(num_seq, num_channels,
+                                                seq_stride, dtype, 1);
+  if (need < 0) return static_cast<int>(need);
+  if (need > kScratchBytes) return ASC_E_SCRATCH;
+  void* ws = nullptr;
+  if (need > 0) {
+    const int st = scratch_ptr(stream, &ws);
+    if (st) return st;
+  }
+  const void* g[1] = {gates};
+  const void* x[1] = {tokens};
+  void* h[1] = {h_out};
+  return run_fwd(g, x, h, gate_prod_out, 1, reverse ? 2 : 1, cu_seqlens,
+                 cu_dtype, num_seq, num_channels, seq_stride, dtype, ws,
+                 need > 0 ? kScratchBytes : 0, stream);
 }
 
 int asc_scan_bwd(const void* grad, const void* gates, const void* states,

@@ -61,11 +61,13 @@ enum {
   ASC_E_DTYPE = -2,      /* unknown dtype / cu dtype                      */
   ASC_E_SIZE = -3,       /* negative or overflowing sizes                 */
   ASC_E_ALIGN = -4,      /* a pointer is not aligned to its element size  */
-  ASC_E_ARG = -5         /* any other invalid argument                    */
+  ASC_E_ARG = -5,        /* any other invalid argument                    */
+  ASC_E_SCRATCH = -6     /* asc_scan_fwd_noalloc: geometry needs more
+                            workspace than its static buffer holds        */
 };
 
 /* ABI version of this header; bumped on any signature change. */
-#define ASC_ABI_VERSION 3
+#define ASC_ABI_VERSION 4
 int asc_abi_version(void);
 
 /*
@@ -130,6 +132,32 @@ int asc_scan_fwd(const void* gates, const void* tokens, void* h_out,
                  int64_t num_seq, int64_t num_channels, int64_t seq_stride,
                  int dtype, int reverse, void* workspace,
                  int64_t workspace_bytes, void* stream);
+
+/*
+ * asc_scan_fwd without a workspace argument and without any allocation:
+ * the look-back and chained walks take their carry slots from a static
+ * device array of 8 MiB that the library holds on each GPU it runs on
+ * until the process ends (looked up once per device, with hipGetSymbolAddress,
+ * on the first call).  Same arguments, results and aliasing rule as
+ * asc_scan_fwd given a workspace of asc_scan_workspace_bytes(); a geometry
+ * that would need more than 8 MiB of workspace returns ASC_E_SCRATCH
+ * (nothing is launched).  `stream` must belong to the current device
+ * (ASC_E_ARG otherwise).  Every call on one GPU shares that GPU's array:
+ * calls that overlap in time on one GPU (other streams, other host threads)
+ * race, so the caller serialises them.  The array keeps the last call's
+ * contents; each call clears the slots it uses on `stream` with a kernel
+ * (no memset, so the call can be captured in a HIP graph).
+ *
+ * No reference counterpart: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc), which with asc_scan_fwd could only pass NULL and lose the
+ * look-back and chained walks.
+ */
+int asc_scan_fwd_noalloc(const void* gates, const void* tokens, void* h_out,
+                         void* gate_prod_out, const void* cu_seqlens,
+                         int cu_dtype, int64_t num_seq, int64_t num_channels,
+                         int64_t seq_stride, int dtype, int reverse,
+                         void* stream);
 
 /*
  * Fused backward of a forward scan (reads dy, g, h once; writes dx, dg).

@@ -39,9 +39,9 @@ def test_exports_every_declared_symbol():
 
 def test_abi_version_and_strerror():
   lib = _lib.load()
-  assert lib.asc_abi_version() == 3
+  assert lib.asc_abi_version() == 4
   assert lib.asc_strerror(0) == b"success"
-  for code in (-1, -2, -3, -4, -5):
+  for code in (-1, -2, -3, -4, -5, -6):
     assert lib.asc_strerror(code) and lib.asc_strerror(code) != b"unknown error"
   assert lib.asc_strerror(-99) == b"unknown error"
 
@@ -196,3 +196,19 @@ def test_aliasing_rule_codes():
   inplace = list(base)
   inplace[4], inplace[5] = inplace[1], inplace[3]   # each branch in place
   assert lib.asc_scan_bidi_fwd(*inplace) == 0
+
+
+def test_noalloc_forward_limits():
+  """asc_scan_fwd_noalloc validates on the host before any HIP call: a
+  geometry whose workspace would exceed its 8 MiB static buffer is
+  ASC_E_SCRATCH, an empty problem is a successful no-op."""
+  lib = _lib.load()
+  # 4096 rows of 256 chunk-aligned 4096-element chunks: 16 MiB of slots
+  assert lib.asc_scan_workspace_bytes(8, 4096, 1 << 20, 0, 1) > 8 << 20
+  assert lib.asc_scan_fwd_noalloc(64, 128, 192, None, 8, 0, 8, 4096, 1 << 20,
+                                  0, 0, None) == -6
+  assert b"8 MiB" in lib.asc_strerror(-6)
+  assert lib.asc_scan_fwd_noalloc(64, 128, 192, None, 8, 0, 0, 1, 4, 0, 0,
+                                  None) == 0
+  assert lib.asc_scan_fwd_noalloc(64, 128, 64, None, 8, 0, 0, 1, 4, 0, 0,
+                                  None) == -5
