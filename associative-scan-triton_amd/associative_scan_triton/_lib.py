@@ -17,7 +17,7 @@ from associative_scan_triton._build import LIB_PATH
 
 ASC_F32, ASC_F16, ASC_BF16 = 0, 1, 2
 ASC_CU_I32, ASC_CU_I64 = 0, 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _DTYPES = {
   torch.float32: ASC_F32,
@@ -42,6 +42,9 @@ SIGNATURES = {
   "asc_scan_fwd": [_P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P, _L, _P],
   "asc_scan_fwd_noalloc": [_P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P],
   "asc_scan_bwd": [_P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P, _L, _P],
+  "asc_scan_checkpoint_elems": [_L, _L, _I],
+  "asc_scan_checkpoints": [_P, _P, _P, _I, _L, _L, _L, _I, _I, _P],
+  "asc_scan_bwd_recompute": [_P, _L, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P, _L, _P],
   "asc_scan_bwd_rowgrad": [_P, _L, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _I, _P, _L, _P],
   "asc_scan_bidi_fwd": [_P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _P, _L, _P],
   "asc_scan_bidi_bwd": [_P] * 11 + [_I, _L, _L, _L, _I, _P, _L, _P],
@@ -55,6 +58,7 @@ WALK_CHAINED = 2
 RESTYPES = {
   "asc_strerror": ctypes.c_char_p,
   "asc_scan_workspace_bytes": ctypes.c_int64,
+  "asc_scan_checkpoint_elems": ctypes.c_int64,
   "asc_set_lookback_spin_limit": ctypes.c_uint,
 }
 

@@ -312,6 +312,112 @@ def scan_bidi_bwd_any(dyf: torch.Tensor | None, dyb: torch.Tensor | None,
                 num_channels)
 
 
+# ---------------------------------------------------------------------------
+# recompute mode: the backward recomputes the forward states from its inputs
+# ---------------------------------------------------------------------------
+
+def checkpoint_shape(tokens: torch.Tensor, num_channels: int | None = None
+                     ) -> tuple[int, int]:
+  """[C, chunks per row] of the checkpoints of a [C, T] tensor (one fp32
+  value per 4096 fp32 / 8192 fp16-bf16 elements of each row)."""
+  C = int(num_channels) if num_channels is not None else (
+    tokens.shape[0] if tokens.dim() == 2 else 1)
+  if C <= 0 or tokens.numel() % C:
+    raise ValueError(
+      f"a tensor of {tokens.numel()} elements cannot hold {C} channels")
+  T = tokens.numel() // C
+  chunk = 4096 if tokens.dtype == torch.float32 else 8192
+  return C, -(-T // chunk)
+
+
+def scan_checkpoints(states: torch.Tensor, cu: torch.Tensor, reverse: bool,
+                     num_channels: int | None = None) -> torch.Tensor:
+  """The forward states the recompute backward starts each chunk from,
+  sampled from a finished forward scan's output (see
+  asc_scan_checkpoints)."""
+  lib = _lib.load()
+  dev = _lib.require_device(states, cu)
+  _check_same(states)
+  dt = _lib.dtype_code(states)
+  cuc = _lib.cu_code(cu)
+  cu = cu.contiguous()
+  S, C, T = _geometry(states, cu, num_channels)
+  ck = torch.empty(checkpoint_shape(states, C), dtype=torch.float32,
+                   device=dev)
+  assert ck.numel() == lib.asc_scan_checkpoint_elems(C, T, dt)
+  with _OnDevice(dev):
+    _lib.check(lib.asc_scan_checkpoints(
+      states.data_ptr(), ck.data_ptr(), cu.data_ptr(), cuc, S, C, T, dt,
+      1 if reverse else 0, _lib.stream_of(dev)))
+  return ck
+
+
+def recompute_in_kernel(gates: torch.Tensor, tokens: torch.Tensor,
+                        cu: torch.Tensor, num_channels: int | None = None
+                        ) -> bool:
+  """Whether the library's recompute backward serves this call: 16-byte
+  aligned tensors, rows a whole number of vectors, and more than a few
+  (segment, channel) items (few items run the look-back walk, which the
+  recompute walks do not replace: those calls recompute the states with the
+  forward scan into a temporary and run the plain backward)."""
+  if gates.data_ptr() % 16 or tokens.data_ptr() % 16:
+    return False
+  S, C, T = _geometry(tokens, cu, num_channels)
+  if T % (16 // tokens.element_size()):
+    return False
+  lib = _lib.load()
+  return lib.asc_scan_workspace_walk(
+    S, C, T, _lib.dtype_code(tokens), 1) != _lib.WALK_LOOKBACK
+
+
+def scan_bwd_recompute(grad: torch.Tensor, gates: torch.Tensor,
+                       tokens: torch.Tensor, ckpt: torch.Tensor | None,
+                       d_tokens: torch.Tensor, d_gates: torch.Tensor,
+                       cu: torch.Tensor, causal: bool,
+                       num_channels: int | None = None) -> None:
+  """Backward of a forward scan of (gates, tokens) without its states:
+  asc_scan_bwd_recompute recomputes them from the checkpoints when
+  recompute_in_kernel() says so (and checkpoints are given); otherwise the
+  states are recomputed into a temporary with the forward scan and the plain
+  backward runs.  A gradient constant along time is read one value per row;
+  None stands for a zero gradient."""
+  if grad is None:
+    grad = tokens.new_zeros(()).expand_as(tokens)
+  if ckpt is None or not recompute_in_kernel(gates, tokens, cu, num_channels):
+    h = torch.empty_like(tokens)
+    scan_fwd(gates, tokens, h, cu, reverse=not causal,
+             num_channels=num_channels)
+    scan_bwd_any(grad, gates, h, d_tokens, d_gates, cu, causal, num_channels)
+    return
+  lib = _lib.load()
+  rs = row_constant_stride(grad, tokens, num_channels)
+  if rs is None:
+    grad = grad.contiguous()
+    rs = -1
+  dev = _lib.require_device(grad, gates, tokens, ckpt, d_tokens, d_gates, cu)
+  _check_same(tokens, gates, d_tokens, d_gates)
+  if grad.dtype != tokens.dtype:
+    raise TypeError(f"dtype mismatch: {tokens.dtype} vs {grad.dtype}")
+  if rs < 0:
+    _check_same(tokens, grad)
+  dt = _lib.dtype_code(tokens)
+  cuc = _lib.cu_code(cu)
+  cu = cu.contiguous()
+  S, C, T = _geometry(tokens, cu, num_channels)
+  if (ckpt.dtype != torch.float32 or not ckpt.is_contiguous()
+      or ckpt.numel() != lib.asc_scan_checkpoint_elems(C, T, dt)):
+    raise ValueError("checkpoints do not match the tensors "
+                     "(see scan_checkpoints)")
+  with _OnDevice(dev):
+    plain = rs >= 0 or d_tokens.data_ptr() != grad.data_ptr()
+    ws, nb = _workspace(lib, dev, S, C, T, dt, 1) if plain else (None, 0)
+    _lib.check(lib.asc_scan_bwd_recompute(
+      grad.data_ptr(), int(rs), gates.data_ptr(), tokens.data_ptr(),
+      ckpt.data_ptr(), d_tokens.data_ptr(), d_gates.data_ptr(), cu.data_ptr(),
+      cuc, S, C, T, dt, 1 if causal else 0, _lib.ptr(ws), nb,
+      _lib.stream_of(dev)))
+
+
 def shift_pad(data: torch.Tensor, out: torch.Tensor, cu: torch.Tensor,
               pad_value: float, backward: bool, wrap: bool) -> None:
   """out <- segment-aware shift of a contiguous [C, L] tensor."""

@@ -200,6 +200,193 @@ scan_bidi_fwd_op.register_autograd(
 )
 
 # ============================================================
+# Recompute mode: the forward ops also return per-chunk checkpoints, and
+# autograd saves (gates, tokens, checkpoints) instead of the outputs; the
+# backward ops recompute the states (see scan_eager.py's recompute_states).
+# The checkpoints are always produced (their shape depends only on the
+# tensors' shapes and dtype), whichever way the backward then recomputes.
+# ============================================================
+
+
+def _ckpt_like(tokens: torch.Tensor, no_channels: int) -> torch.Tensor:
+  return tokens.new_empty(_ops.checkpoint_shape(tokens, no_channels),
+                          dtype=torch.float32)
+
+
+@torch.library.custom_op("associative_scan_triton::scan_causal_fwd_rc",
+                         mutates_args=())
+def scan_causal_fwd_rc_op(
+  gates: torch.Tensor,
+  tokens: torch.Tensor,
+  cu_seqlens: torch.Tensor,
+  num_chunks: int,
+  no_channels: int,
+  chunk_size: int,
+) -> tuple[torch.Tensor, torch.Tensor]:
+  """Causal scan forward; returns (out_tokens, checkpoints)."""
+  out = torch.empty_like(tokens)
+  _ops.scan_fwd(gates, tokens, out, cu_seqlens, reverse=False,
+                num_channels=no_channels)
+  return out, _ops.scan_checkpoints(out, cu_seqlens, False, no_channels)
+
+
+@scan_causal_fwd_rc_op.register_fake
+def _(gates, tokens, cu_seqlens, num_chunks, no_channels, chunk_size):
+  return torch.empty_like(tokens), _ckpt_like(tokens, no_channels)
+
+
+@torch.library.custom_op("associative_scan_triton::scan_causal_bwd_rc",
+                         mutates_args=())
+def scan_causal_bwd_rc_op(
+  grad: torch.Tensor,
+  gates: torch.Tensor,
+  tokens: torch.Tensor,
+  checkpoints: torch.Tensor,
+  cu_seqlens: torch.Tensor,
+  num_chunks: int,
+  no_channels: int,
+  chunk_size: int,
+) -> tuple[torch.Tensor, torch.Tensor]:
+  """Causal scan backward from the forward's inputs and checkpoints;
+  returns (d_gates, d_tokens)."""
+  d_tokens = torch.empty_like(tokens)
+  d_gates = torch.empty_like(gates)
+  _ops.scan_bwd_recompute(grad, gates, tokens, checkpoints, d_tokens, d_gates,
+                          cu_seqlens, causal=True, num_channels=no_channels)
+  return d_gates, d_tokens
+
+
+@scan_causal_bwd_rc_op.register_fake
+def _(grad, gates, tokens, checkpoints, cu_seqlens, num_chunks, no_channels,
+      chunk_size):
+  return torch.empty_like(gates), torch.empty_like(tokens)
+
+
+def _scan_causal_rc_setup_context(ctx, inputs, output) -> None:
+  gates, tokens, cu_seqlens, num_chunks, no_channels, chunk_size = inputs
+  _out, ckpt = output
+  ctx.mark_non_differentiable(ckpt)
+  ctx.set_materialize_grads(False)
+  ctx.save_for_backward(gates, tokens, ckpt)
+  ctx.cu_seqlens = cu_seqlens
+  ctx.num_chunks = num_chunks
+  ctx.no_channels = no_channels
+  ctx.chunk_size = chunk_size
+
+
+def _scan_causal_rc_backward(ctx, grad, _grad_ckpt):
+  gates, tokens, ckpt = ctx.saved_tensors
+  if grad is None:
+    grad = tokens.new_zeros(()).expand_as(tokens)
+  d_gates, d_tokens = scan_causal_bwd_rc_op(
+    grad, gates, tokens, ckpt, ctx.cu_seqlens, ctx.num_chunks,
+    ctx.no_channels, ctx.chunk_size)
+  return d_gates, d_tokens, None, None, None, None
+
+
+scan_causal_fwd_rc_op.register_autograd(
+  _scan_causal_rc_backward, setup_context=_scan_causal_rc_setup_context
+)
+
+
+@torch.library.custom_op("associative_scan_triton::scan_bidi_fwd_rc",
+                         mutates_args=())
+def scan_bidi_fwd_rc_op(
+  gates_fwd: torch.Tensor,
+  tokens_fwd: torch.Tensor,
+  gates_bwd: torch.Tensor,
+  tokens_bwd: torch.Tensor,
+  cu_seqlens: torch.Tensor,
+  num_chunks: int,
+  no_channels: int,
+  chunk_size: int,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+  """Both branches in one launch; returns (out_tokens_fwd, out_tokens_bwd,
+  checkpoints_fwd, checkpoints_bwd)."""
+  out_fwd = torch.empty_like(tokens_fwd)
+  out_bwd = torch.empty_like(tokens_bwd)
+  _ops.scan_bidi_fwd(gates_fwd, tokens_fwd, gates_bwd, tokens_bwd, out_fwd,
+                     out_bwd, cu_seqlens, num_channels=no_channels)
+  return (out_fwd, out_bwd,
+          _ops.scan_checkpoints(out_fwd, cu_seqlens, False, no_channels),
+          _ops.scan_checkpoints(out_bwd, cu_seqlens, True, no_channels))
+
+
+@scan_bidi_fwd_rc_op.register_fake
+def _(gates_fwd, tokens_fwd, gates_bwd, tokens_bwd, cu_seqlens, num_chunks,
+      no_channels, chunk_size):
+  return (torch.empty_like(tokens_fwd), torch.empty_like(tokens_bwd),
+          _ckpt_like(tokens_fwd, no_channels),
+          _ckpt_like(tokens_bwd, no_channels))
+
+
+@torch.library.custom_op("associative_scan_triton::scan_bidi_bwd_rc",
+                         mutates_args=())
+def scan_bidi_bwd_rc_op(
+  grad_fwd: torch.Tensor,
+  grad_bwd: torch.Tensor,
+  gates_fwd: torch.Tensor,
+  tokens_fwd: torch.Tensor,
+  gates_bwd: torch.Tensor,
+  tokens_bwd: torch.Tensor,
+  checkpoints_fwd: torch.Tensor,
+  checkpoints_bwd: torch.Tensor,
+  cu_seqlens: torch.Tensor,
+  num_chunks: int,
+  no_channels: int,
+  chunk_size: int,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+  """Backward of both branches from their inputs and checkpoints; returns
+  (d_gates_fwd, d_tokens_fwd, d_gates_bwd, d_tokens_bwd)."""
+  out = [torch.empty_like(t) for t in
+         (gates_fwd, tokens_fwd, gates_bwd, tokens_bwd)]
+  _ops.scan_bwd_recompute(grad_fwd, gates_fwd, tokens_fwd, checkpoints_fwd,
+                          out[1], out[0], cu_seqlens, causal=True,
+                          num_channels=no_channels)
+  _ops.scan_bwd_recompute(grad_bwd, gates_bwd, tokens_bwd, checkpoints_bwd,
+                          out[3], out[2], cu_seqlens, causal=False,
+                          num_channels=no_channels)
+  return tuple(out)
+
+
+@scan_bidi_bwd_rc_op.register_fake
+def _(grad_fwd, grad_bwd, gates_fwd, tokens_fwd, gates_bwd, tokens_bwd,
+      checkpoints_fwd, checkpoints_bwd, cu_seqlens, num_chunks, no_channels,
+      chunk_size):
+  return (torch.empty_like(gates_fwd), torch.empty_like(tokens_fwd),
+          torch.empty_like(gates_bwd), torch.empty_like(tokens_bwd))
+
+
+def _scan_bidi_rc_setup_context(ctx, inputs, output) -> None:
+  (gates_fwd, tokens_fwd, gates_bwd, tokens_bwd,
+   cu_seqlens, num_chunks, no_channels, chunk_size) = inputs
+  _of, _ob, ckf, ckb = output
+  ctx.mark_non_differentiable(ckf, ckb)
+  ctx.set_materialize_grads(False)
+  ctx.save_for_backward(gates_fwd, tokens_fwd, gates_bwd, tokens_bwd, ckf, ckb)
+  ctx.cu_seqlens = cu_seqlens
+  ctx.num_chunks = num_chunks
+  ctx.no_channels = no_channels
+  ctx.chunk_size = chunk_size
+
+
+def _scan_bidi_rc_backward(ctx, grad_fwd, grad_bwd, _gcf, _gcb):
+  gf, tf, gb, tb, ckf, ckb = ctx.saved_tensors
+  if grad_fwd is None:
+    grad_fwd = tf.new_zeros(()).expand_as(tf)
+  if grad_bwd is None:
+    grad_bwd = tb.new_zeros(()).expand_as(tb)
+  d = scan_bidi_bwd_rc_op(grad_fwd, grad_bwd, gf, tf, gb, tb, ckf, ckb,
+                          ctx.cu_seqlens, ctx.num_chunks, ctx.no_channels,
+                          ctx.chunk_size)
+  return (*d, None, None, None, None)
+
+
+scan_bidi_fwd_rc_op.register_autograd(
+  _scan_bidi_rc_backward, setup_context=_scan_bidi_rc_setup_context
+)
+
+# ============================================================
 # Public API (scan_compiled.py:333-371)
 # ============================================================
 
@@ -208,11 +395,15 @@ def scan_causal_compiled(
   gates: torch.Tensor,
   tokens: torch.Tensor,
   args: dict,
+  recompute_states: bool = False,
 ) -> torch.Tensor:
   """Drop-in replacement for scan_causal() built on a custom op."""
   cu_seqlens = args["cu_seqlens"]
   chunk_size = args["chunk_size"]
   _num_seq, num_chunks, no_channels = args["grid"]
+  if recompute_states:
+    return scan_causal_fwd_rc_op(
+      gates, tokens, cu_seqlens, num_chunks, no_channels, chunk_size)[0]
   return scan_causal_fwd_op(
     gates, tokens, cu_seqlens, num_chunks, no_channels, chunk_size,
   )
@@ -225,12 +416,17 @@ def scan_bidirectional_branched_compiled(
   tokens_bwd: torch.Tensor,
   args: dict,
   testing: bool = True,
+  recompute_states: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor]:
   """Drop-in replacement for scan_bidirectional_branched() on custom ops."""
   del testing
   cu_seqlens = args["cu_seqlens"]
   chunk_size = args["chunk_size"]
   _num_seq, num_chunks, no_channels = args["grid"]
+  if recompute_states:
+    return scan_bidi_fwd_rc_op(
+      gates_fwd, tokens_fwd, gates_bwd, tokens_bwd,
+      cu_seqlens, num_chunks, no_channels, chunk_size)[:2]
   return scan_bidi_fwd_op(
     gates_fwd, tokens_fwd, gates_bwd, tokens_bwd,
     cu_seqlens, num_chunks, no_channels, chunk_size,

@@ -4,6 +4,15 @@ Same public functions, argument meaning, saved tensors and gradient order
 as the reference.  Differences are internal: the bidirectional scan runs
 both branches in one launch forward and one launch backward instead of two
 each.
+
+Addition: ``recompute_states=True`` (default False) keeps the forward's
+inputs and one fp32 checkpoint per 4096 fp32 / 8192 fp16-bf16 elements of
+each row for the backward instead of the scanned output, which the
+backward then recomputes chunk by chunk in registers (no [C, T] tensor of
+states is kept alive between the forward and the backward; the backward's
+HBM traffic is unchanged).  Results agree with the default mode to the
+dtype's rounding.  The reference lists this as future work (the
+recompute-states backward; it saves the outputs, scan_eager.py:42-47).
 """
 
 from __future__ import annotations
@@ -21,7 +30,7 @@ class ScanCausal(torch.autograd.Function):
   """Causal (unidirectional) scan with autograd (scan_eager.py:20-64)."""
 
   @staticmethod
-  def forward(ctx, gates, tokens, args) -> torch.Tensor:
+  def forward(ctx, gates, tokens, args, recompute_states=False) -> torch.Tensor:
     shape = gates.shape
     assert tokens.shape == shape
     assert gates.is_contiguous()
@@ -40,11 +49,24 @@ class ScanCausal(torch.autograd.Function):
       ctx.grid = grid
       ctx.cu_seqlens = cu_seqlens
       ctx.chunk_size = chunk_size
-      ctx.save_for_backward(out_tokens, gates)
+      ctx.recompute = bool(recompute_states)
+      if ctx.recompute:
+        ckpt = _checkpoints(gates, tokens, out_tokens, cu_seqlens, False, grid[2])
+        ctx.save_for_backward(gates, tokens, ckpt)
+      else:
+        ctx.save_for_backward(out_tokens, gates)
     return out_tokens
 
   @staticmethod
   def backward(ctx, grad_output):
+    if ctx.recompute:
+      gates, tokens, ckpt = ctx.saved_tensors
+      d_tokens = torch.empty_like(tokens)
+      d_gates = torch.empty_like(gates)
+      _ops.scan_bwd_recompute(grad_output, gates, tokens, ckpt, d_tokens,
+                              d_gates, ctx.cu_seqlens, causal=True,
+                              num_channels=ctx.grid[2])
+      return d_gates, d_tokens, None, None
     states, gates = ctx.saved_tensors
     # A gradient constant along time (out.sum()) is read one value per row
     # instead of being materialised (the reference's .contiguous(),
@@ -53,13 +75,23 @@ class ScanCausal(torch.autograd.Function):
     d_gates = torch.empty_like(gates)
     _ops.scan_bwd_any(grad_output, gates, states, d_tokens, d_gates,
                       ctx.cu_seqlens, causal=True, num_channels=ctx.grid[2])
-    return d_gates, d_tokens, None
+    return d_gates, d_tokens, None, None
+
+
+def _checkpoints(gates, tokens, states, cu_seqlens, reverse, num_channels):
+  """Checkpoints for the recompute backward, or None when the backward will
+  recompute the states with the forward scan instead (few items, unaligned
+  tensors)."""
+  if not _ops.recompute_in_kernel(gates, tokens, cu_seqlens, num_channels):
+    return None
+  return _ops.scan_checkpoints(states, cu_seqlens, reverse, num_channels)
 
 
 def scan_causal(
   gates: torch.Tensor,
   tokens: torch.Tensor,
   args: dict,
+  recompute_states: bool = False,
 ) -> torch.Tensor:
   """Causal associative scan ``h[t] = gates[t]*h[t-1] + tokens[t]``.
 
@@ -68,11 +100,13 @@ def scan_causal(
     tokens: [C, B*L] token values
     args: dict with keys "cu_seqlens" ([B+1] cumulative lengths),
       "chunk_size" (int) and "grid" ((num_seq, num_chunks, no_channels)).
+    recompute_states: keep (gates, tokens) and per-chunk checkpoints for the
+      backward instead of the output, and recompute the states there.
 
   Returns:
     scanned tokens, [C, B*L]
   """
-  return ScanCausal.apply(gates, tokens, args)
+  return ScanCausal.apply(gates, tokens, args, recompute_states)
 
 
 class ScanBidirectionalBranched(torch.autograd.Function):
@@ -80,7 +114,7 @@ class ScanBidirectionalBranched(torch.autograd.Function):
 
   @staticmethod
   def forward(ctx, gates_fwd, tokens_fwd, gates_bwd, tokens_bwd, args,
-              testing=False):
+              testing=False, recompute_states=False):
     shape = gates_fwd.shape
     assert tokens_fwd.shape == shape
     assert tokens_bwd.shape == shape
@@ -108,9 +142,18 @@ class ScanBidirectionalBranched(torch.autograd.Function):
       ctx.cu_seqlens = cu_seqlens
       ctx.chunk_size = chunk_size
       ctx.testing = testing
-      ctx.save_for_backward(
-        out_tokens_fwd, out_tokens_bwd, gates_fwd, gates_bwd
-      )
+      ctx.recompute = bool(recompute_states)
+      if ctx.recompute:
+        ckf = _checkpoints(gates_fwd, tokens_fwd, out_tokens_fwd, cu_seqlens,
+                           False, grid[2])
+        ckb = _checkpoints(gates_bwd, tokens_bwd, out_tokens_bwd, cu_seqlens,
+                           True, grid[2])
+        ctx.save_for_backward(gates_fwd, tokens_fwd, gates_bwd, tokens_bwd,
+                              ckf, ckb)
+      else:
+        ctx.save_for_backward(
+          out_tokens_fwd, out_tokens_bwd, gates_fwd, gates_bwd
+        )
     # an output that receives no gradient arrives as None (a zero gradient
     # read as one value, not a materialised zeros tensor)
     ctx.set_materialize_grads(False)
@@ -118,6 +161,16 @@ class ScanBidirectionalBranched(torch.autograd.Function):
 
   @staticmethod
   def backward(ctx, grad_output_fwd, grad_output_bwd):
+    if ctx.recompute:
+      gf, tf, gb, tb, ckf, ckb = ctx.saved_tensors
+      out = [torch.empty_like(t) for t in (gf, tf, gb, tb)]
+      _ops.scan_bwd_recompute(grad_output_fwd, gf, tf, ckf, out[1], out[0],
+                              ctx.cu_seqlens, causal=True,
+                              num_channels=ctx.grid[2])
+      _ops.scan_bwd_recompute(grad_output_bwd, gb, tb, ckb, out[3], out[2],
+                              ctx.cu_seqlens, causal=False,
+                              num_channels=ctx.grid[2])
+      return (*out, None, None, None)
     states_fwd, states_bwd, gates_fwd, gates_bwd = ctx.saved_tensors
     # gradients constant along time (out.sum()) are read one value per row;
     # any other layout is made contiguous, as the reference does
@@ -136,6 +189,7 @@ class ScanBidirectionalBranched(torch.autograd.Function):
       d_tokens_bwd,
       None,  # args
       None,  # testing
+      None,  # recompute_states
     )
 
 
@@ -146,14 +200,17 @@ def scan_bidirectional_branched(
   tokens_bwd: torch.Tensor,
   args: dict,
   testing: bool = True,
+  recompute_states: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor]:
   """Bidirectional branched scan: causal over the forward pair, reverse over
   the backward pair.  ``testing`` is accepted and, as in the reference
-  (scan_eager.py:137), has no effect on the results.
+  (scan_eager.py:137), has no effect on the results; ``recompute_states`` as
+  for scan_causal, per branch.
 
   Returns:
     (scanned_tokens_fwd, scanned_tokens_bwd)
   """
   return ScanBidirectionalBranched.apply(
-    gates_fwd, tokens_fwd, gates_bwd, tokens_bwd, args, testing
+    gates_fwd, tokens_fwd, gates_bwd, tokens_bwd, args, testing,
+    recompute_states
   )

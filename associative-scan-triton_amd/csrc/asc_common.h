@@ -848,6 +848,34 @@ bool chain_bwd(const BwdParams& p, int dtype, bool aln, bool dyc, int dirs,
                void* ws, int64_t ws_bytes, void* stream, int& status,
                const uint32_t** skip);
 
+// scan_recompute.hip: the backward that recomputes the forward states from
+// its inputs and per-chunk checkpoints (asc_scan_bwd_recompute).
+// rc_chunks_per_row: checkpoints per row; rc_checkpoints samples them from
+// the forward's states; rc_bwd launches the recompute walks (arguments
+// already validated; phase 0 and T a multiple of the vector width).
+struct RcArgs {
+  const void* dy;
+  int64_t dy_rs;  // < 0: dy is a dense [C, T] tensor; else one value per row
+  const void* g;
+  const void* x;
+  const float* ckpt;
+  void* dx;
+  void* dg;
+  const void* cu;
+  int cu64;
+  int64_t S, C, T;
+  int dtype;
+  bool causal;
+  bool inplace;  // dx is dy: only the per-item walk
+  void* ws;
+  int64_t ws_bytes;
+};
+int64_t rc_chunks_per_row(int64_t T, int v);
+int rc_checkpoints(const void* h, float* ckpt, const void* cu, int cu_dtype,
+                   int64_t S, int64_t C, int64_t T, int dtype, int reverse,
+                   void* stream);
+int rc_bwd(const RcArgs& a, void* stream);
+
 }  // namespace asc
 
 #endif  // ASC_COMMON_H

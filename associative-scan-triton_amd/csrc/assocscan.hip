@@ -333,6 +333,91 @@ int asc_scan_fwd_noalloc(const void* gates, const void* tokens, void* h_out,
                  need > 0 ? kScratchBytes : 0, stream);
 }
 
+int64_t asc_scan_checkpoint_elems(int64_t num_channels, int64_t seq_stride,
+                                  int dtype) {
+  const int es = elem_size(dtype);
+  if (es == 0 || num_channels < 0 || seq_stride < 0) return ASC_E_ARG;
+  const int64_t kr = rc_chunks_per_row(seq_stride, 16 / es);
+  if (kr > 0 && num_channels > INT64_MAX / kr) return ASC_E_SIZE;
+  return num_channels * kr;
+}
+
+int asc_scan_checkpoints(const void* states, float* checkpoints,
+                         const void* cu_seqlens, int cu_dtype, int64_t num_seq,
+                         int64_t num_channels, int64_t seq_stride, int dtype,
+                         int reverse, void* stream) {
+  int st = check_geometry(cu_seqlens, cu_dtype, num_seq, num_channels,
+                          seq_stride, dtype);
+  if (st) return st;
+  if (!states || !checkpoints) return ASC_E_NULL;
+  const int es = elem_size(dtype);
+  const void* p[1] = {states};
+  if ((st = check_ptrs(p, 1, es))) return st;
+  if (reinterpret_cast<uintptr_t>(checkpoints) % 4) return ASC_E_ALIGN;
+  const int64_t nck = asc_scan_checkpoint_elems(num_channels, seq_stride, dtype);
+  if (overlap(states, num_channels * seq_stride * es, checkpoints, nck * 4))
+    return ASC_E_ARG;
+  if (nck == 0) return ASC_OK;
+  return rc_checkpoints(states, checkpoints, cu_seqlens, cu_dtype, num_seq,
+                        num_channels, seq_stride, dtype, reverse, stream);
+}
+
+int asc_scan_bwd_recompute(const void* grad, int64_t grad_row_stride,
+                           const void* gates, const void* tokens,
+                           const float* checkpoints, void* d_tokens,
+                           void* d_gates, const void* cu_seqlens, int cu_dtype,
+                           int64_t num_seq, int64_t num_channels,
+                           int64_t seq_stride, int dtype, int causal,
+                           void* workspace, int64_t workspace_bytes,
+                           void* stream) {
+  const int64_t S = num_seq, C = num_channels, T = seq_stride;
+  int st = check_geometry(cu_seqlens, cu_dtype, S, C, T, dtype);
+  if (st) return st;
+  if (!grad || !gates || !tokens || !checkpoints || !d_tokens || !d_gates)
+    return ASC_E_NULL;
+  const int es = elem_size(dtype);
+  const int v = 16 / es;
+  const bool dense = grad_row_stride < 0;
+  const void* all[5] = {gates, tokens, d_tokens, d_gates, grad};
+  if ((st = check_ptrs(all, 5, es))) return st;
+  if (reinterpret_cast<uintptr_t>(checkpoints) % 4) return ASC_E_ALIGN;
+  // the recompute walks address whole 16-byte vectors of every row
+  for (int i = 0; i < (dense ? 5 : 4); ++i)
+    if (reinterpret_cast<uintptr_t>(all[i]) % 16) return ASC_E_ALIGN;
+  if (T % v) return ASC_E_ALIGN;
+  const int64_t nbytes = C * T * es;
+  const int64_t gbytes =
+      dense ? nbytes : ((C > 0 ? C - 1 : 0) * grad_row_stride + 1) * es;
+  const int64_t nck = asc_scan_checkpoint_elems(C, T, dtype);
+  if (nck < 0) return static_cast<int>(nck);
+  const OutArg outs[2] = {{d_tokens, nbytes, dense ? grad : nullptr},
+                          {d_gates, nbytes, nullptr}};
+  const InArg ins[4] = {{grad, gbytes}, {gates, nbytes}, {tokens, nbytes},
+                        {checkpoints, nck * 4}};
+  bool inplace = false;
+  if ((st = check_alias(outs, 2, ins, 4, &inplace))) return st;
+  if (S == 0 || C == 0 || T == 0) return ASC_OK;
+  RcArgs a{};
+  a.dy = grad;
+  a.dy_rs = grad_row_stride;
+  a.g = gates;
+  a.x = tokens;
+  a.ckpt = checkpoints;
+  a.dx = d_tokens;
+  a.dg = d_gates;
+  a.cu = cu_seqlens;
+  a.cu64 = cu_dtype == ASC_CU_I64;
+  a.S = S;
+  a.C = C;
+  a.T = T;
+  a.dtype = dtype;
+  a.causal = causal != 0;
+  a.inplace = inplace;
+  a.ws = workspace;
+  a.ws_bytes = workspace_bytes;
+  return rc_bwd(a, stream);
+}
+
 int asc_scan_bwd(const void* grad, const void* gates, const void* states,
                  void* d_tokens, void* d_gates, const void* cu_seqlens,
                  int cu_dtype, int64_t num_seq, int64_t num_channels,

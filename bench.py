@@ -77,6 +77,8 @@ def parse():
   p.add_argument("--no-check", action="store_true")
   p.add_argument("--no-api", action="store_true",
                  help="skip the API-level (autograd, out.sum()) timing")
+  p.add_argument("--no-recompute", action="store_true",
+                 help="skip the recompute-mode legs (kernel and API level)")
   p.add_argument("--profile-copy", action="store_true",
                  help="also launch one plain device copy of one tensor "
                       "(rocprof byte-counter calibration)")
@@ -327,6 +329,107 @@ def main():
     del leaves
     log(f"[bench] api level: {api}")
 
+  # ---- recompute mode (causal configs): the backward reads (dy, g, x) and
+  # per-chunk checkpoints instead of (dy, g, h).  Kernel level: forward +
+  # checkpoints, then the recompute backward, K steps back to back; API
+  # level: scan_causal(..., recompute_states=True).sum().backward() against
+  # the default mode, with the memory each keeps between the forward and the
+  # backward and the peak over the step (above what was allocated before) ----
+  recompute = None
+  if (with_bwd and kind == "causal" and not a.no_recompute
+      and _ops.recompute_in_kernel(g[0], x[0], cu)):
+    import associative_scan_triton as ast
+
+    def fwd_rc():
+      _ops.scan_fwd(g[0], x[0], h[0], cu, reverse=False)
+      return _ops.scan_checkpoints(h[0], cu, reverse=False)
+
+    ck = fwd_rc()
+
+    def bwd_rc():
+      _ops.scan_bwd_recompute(dy[0], g[0], x[0], ck, dx[0], dg[0], cu,
+                              causal=True)
+
+    for _ in range(a.warmup):
+      fwd_rc()
+      bwd_rc()
+    torch.cuda.synchronize()
+    evr = [[torch.cuda.Event(enable_timing=True) for _ in range(3)]
+           for _ in range(a.steps)]
+    for k in range(a.steps):
+      evr[k][0].record(stream)
+      fwd_rc()
+      evr[k][1].record(stream)
+      bwd_rc()
+      evr[k][2].record(stream)
+    torch.cuda.synchronize()
+    rf = float(np.mean([e[0].elapsed_time(e[1]) for e in evr]))
+    rb = float(np.mean([e[1].elapsed_time(e[2]) for e in evr]))
+    args_rc = {"cu_seqlens": cu, "chunk_size": 128,
+               "grid": ast.get_grid(B + 1, int((cu[1:] - cu[:-1]).max()), 128, C)}
+    gl = g[0].detach().requires_grad_(True)
+    xl = x[0].detach().requires_grad_(True)
+
+    def api_mode(rc):
+      def step():
+        gl.grad = xl.grad = None
+        loss = ast.scan_causal(gl, xl, args_rc, recompute_states=rc).sum()
+        loss.backward()
+      for _ in range(a.warmup):
+        step()
+      torch.cuda.synchronize()
+      e0 = torch.cuda.Event(enable_timing=True)
+      e1 = torch.cuda.Event(enable_timing=True)
+      e0.record(stream)
+      for _ in range(a.steps):
+        step()
+      e1.record(stream)
+      torch.cuda.synchronize()
+      ms = e0.elapsed_time(e1) / a.steps
+      gl.grad = xl.grad = None
+      torch.cuda.synchronize()
+      base = torch.cuda.memory_allocated()
+      torch.cuda.reset_peak_memory_stats()
+      loss = ast.scan_causal(gl, xl, args_rc, recompute_states=rc).sum()
+      torch.cuda.synchronize()
+      held = torch.cuda.memory_allocated() - base
+      loss.backward()
+      torch.cuda.synchronize()
+      peak = torch.cuda.max_memory_allocated() - base
+      gl.grad = xl.grad = None
+      del loss
+      return {"ms_per_step": round(ms, 4),
+              "held_between_fwd_and_bwd_bytes": int(held),
+              "peak_above_inputs_bytes": int(peak)}
+
+    recompute = {
+      "what": "backward from (dy, g, x) + per-chunk checkpoints instead of "
+              "(dy, g, h): scan_causal(..., recompute_states=True)",
+      "kernel_fwd_ms": round(rf, 4), "kernel_bwd_ms": round(rb, 4),
+      "kernel_fwd_bwd_ms": round(rf + rb, 4),
+      "kernel_bwd_GBs": round(bwd_bytes / (rb * 1e-3) / 1e9, 2),
+      "checkpoint_bytes": int(ck.numel() * 4),
+      "api_default": api_mode(False), "api_recompute": api_mode(True)}
+    if not a.no_check:
+      from oracle import oracle
+      rows = sorted({0, C // 2, C - 1})
+      cu_np = cu.cpu().numpy().astype(np.int64)
+      gs = g[0][rows].double().cpu().numpy()
+      hs = h[0][rows].double().cpu().numpy()   # the stored states
+      dxr, dgr = oracle.scan_bwd(dy[0][rows].double().cpu().numpy(), gs, hs,
+                                 cu_np, causal=True)
+      tol = 1e-5 if dtype == torch.float32 else 1e-2
+
+      def ratio(got, ref):
+        s_ = max(1.0, float(np.sqrt(np.mean(ref * ref))))
+        return float(np.max(np.abs(got - ref) / (tol * s_ + tol * np.abs(ref))))
+
+      recompute["check_max_err_over_bound"] = {
+        "dx": ratio(dx[0][rows].double().cpu().numpy(), dxr),
+        "dg": ratio(dg[0][rows].double().cpu().numpy(), dgr)}
+    del gl, xl
+    log(f"[bench] recompute mode: {recompute}")
+
   traffic = None
   tf = ROOT / "profiles" / f"traffic_{a.config}.json"
   if tf.exists():
@@ -359,6 +462,7 @@ def main():
                  "algorithmic_bytes": dom_bytes},
     "cpu_baseline": cpu,
     "api": api,
+    "recompute": recompute,
     "check": check,
   }
   if a.config == "cfg5":

@@ -67,7 +67,7 @@ enum {
 };
 
 /* ABI version of this header; bumped on any signature change. */
-#define ASC_ABI_VERSION 4
+#define ASC_ABI_VERSION 5
 int asc_abi_version(void);
 
 /*
@@ -206,6 +206,57 @@ int asc_scan_bwd_rowgrad(const void* grad_rows, int64_t grad_row_stride,
                          int64_t seq_stride, int dtype, int causal,
                          void* workspace, int64_t workspace_bytes,
                          void* stream);
+
+/*
+ * Recompute mode (an opt-in of the autograd functions that keeps the
+ * forward's inputs instead of its output for the backward).
+ *
+ * Checkpoints: one fp32 value per chunk of each row, chunks of 4096 (fp32)
+ * or 8192 (fp16, bf16) elements along the row, the last one partial when
+ * the row is not a whole number of chunks; asc_scan_checkpoint_elems(C, T,
+ * dtype) = C * ceil(T / chunk) of them.  asc_scan_checkpoints samples them
+ * from the states h of a finished forward scan (reverse = that scan's
+ * direction): checkpoint (c, k) is the state adjacent to chunk k on the side
+ * the scan comes from (causal: element k*chunk - 1 of row c; reverse: the
+ * element just after the chunk) when it lies in the same segment as the
+ * chunk's first element in scan order, else 0.
+ *
+ * asc_scan_bwd_recompute is asc_scan_bwd (causal = 1: the backward of
+ * reverse = 0) reading the forward's tokens and the checkpoints instead of
+ * the states: it recomputes the states chunk by chunk in registers, rounds
+ * them to the storage type, and writes d_tokens and d_gates; HBM traffic is
+ * that of asc_scan_bwd (dy, g, x read once; dx, dg written once).
+ * grad_row_stride < 0: grad is a dense [C, T] tensor; >= 0: one value per
+ * row, grad[c * grad_row_stride], as in asc_scan_bwd_rowgrad.  Every tensor
+ * (and the dense gradient) must be 16-byte aligned and T a multiple of 4
+ * (fp32) or 8 (fp16, bf16) elements, else ASC_E_ALIGN.  The workspace (as
+ * asc_scan_workspace_bytes(..., nbranch = 1) says) buys the chained walk for
+ * chunk-aligned segments; without it, for unaligned segments and for any
+ * other geometry one workgroup per (segment, channel) item walks the chunks
+ * (correct for every geometry, but slow for problems with few items, which
+ * callers serve better by recomputing the states with asc_scan_fwd and
+ * calling asc_scan_bwd).  Aliasing as asc_scan_bwd (d_tokens may equal a
+ * dense grad; the checkpoints are an input).
+ *
+ * Replaces: scan_eager.py:42-47 and :50-64 (the states saved for the
+ * backward, and backward_scan_fused_full on them) for callers that trade
+ * the recompute for one [C, T] tensor of memory per call; the reference
+ * lists it as future work (the recompute-states backward).
+ */
+int64_t asc_scan_checkpoint_elems(int64_t num_channels, int64_t seq_stride,
+                                  int dtype);
+int asc_scan_checkpoints(const void* states, float* checkpoints,
+                         const void* cu_seqlens, int cu_dtype, int64_t num_seq,
+                         int64_t num_channels, int64_t seq_stride, int dtype,
+                         int reverse, void* stream);
+int asc_scan_bwd_recompute(const void* grad, int64_t grad_row_stride,
+                           const void* gates, const void* tokens,
+                           const float* checkpoints, void* d_tokens,
+                           void* d_gates, const void* cu_seqlens, int cu_dtype,
+                           int64_t num_seq, int64_t num_channels,
+                           int64_t seq_stride, int dtype, int causal,
+                           void* workspace, int64_t workspace_bytes,
+                           void* stream);
 
 /*
  * Both branches of the bidirectional scan in ONE launch: a causal scan of

@@ -39,7 +39,7 @@ def test_exports_every_declared_symbol():
 
 def test_abi_version_and_strerror():
   lib = _lib.load()
-  assert lib.asc_abi_version() == 4
+  assert lib.asc_abi_version() == 5
   assert lib.asc_strerror(0) == b"success"
   for code in (-1, -2, -3, -4, -5, -6):
     assert lib.asc_strerror(code) and lib.asc_strerror(code) != b"unknown error"
@@ -212,3 +212,39 @@ def test_noalloc_forward_limits():
                                   None) == 0
   assert lib.asc_scan_fwd_noalloc(64, 128, 64, None, 8, 0, 0, 1, 4, 0, 0,
                                   None) == -5
+
+
+def test_recompute_entry_points_validation():
+  """Checkpoint counts and the recompute backward's host-side checks: whole
+  16-byte vectors (aligned tensors, rows a multiple of the vector width),
+  the aliasing rule (the checkpoints are an input); S = 0 launches nothing."""
+  lib = _lib.load()
+  ce = lib.asc_scan_checkpoint_elems
+  assert ce(1536, 524288, 0) == 1536 * 128          # 4096 fp32 per chunk
+  assert ce(1536, 524288, 2) == 1536 * 64           # 8192 bf16 per chunk
+  assert ce(3, 4097, 0) == 3 * 2 and ce(3, 4096, 0) == 3 and ce(3, 0, 0) == 0
+  assert ce(3, 10, 9) < 0 and ce(-1, 10, 0) < 0
+
+  def rc(grad=64, rs=-1, gates=128, tokens=192, ckpt=256, dx=320, dg=384,
+         S=0, C=1, T=4, dtype=0):
+    return lib.asc_scan_bwd_recompute(grad, rs, gates, tokens, ckpt, dx, dg,
+                                      8, 0, S, C, T, dtype, 1, None, 0, None)
+
+  assert rc() == 0
+  assert rc(dx=64) == 0               # d_tokens over the dense gradient
+  assert rc(dx=256) == -5             # over the checkpoints
+  assert rc(dg=192) == -5             # over the tokens
+  assert rc(rs=0, grad=68, dx=64) == -5   # the row gradient is not replaced
+  assert rc(tokens=200) == -4         # not 16-byte aligned
+  assert rc(grad=72) == -4            # a dense gradient must be aligned too
+  assert rc(grad=72, rs=0) == 0       # one value per row need not be
+  assert rc(T=6) == -4                # rows not a whole number of vectors
+  assert rc(T=8, dtype=2) == 0 and rc(T=12, dtype=2) == -4
+  assert rc(ckpt=258) == -4
+  assert rc(gates=None) == -1 and rc(ckpt=None) == -1
+  # C = 0: no checkpoints, nothing launched (with rows, S = 0 still writes
+  # zero checkpoints)
+  assert lib.asc_scan_checkpoints(64, 128, 8, 0, 0, 0, 4, 0, 0, None) == 0
+  assert lib.asc_scan_checkpoints(64, 66, 8, 0, 0, 1, 4, 0, 0, None) == -4
+  assert lib.asc_scan_checkpoints(64, 72, 8, 0, 0, 1, 4, 0, 0, None) == -5
+  assert lib.asc_scan_checkpoints(None, 128, 8, 0, 0, 1, 4, 0, 0, None) == -1
