@@ -355,19 +355,20 @@ def scan_checkpoints(states: torch.Tensor, cu: torch.Tensor, reverse: bool,
 def recompute_in_kernel(gates: torch.Tensor, tokens: torch.Tensor,
                         cu: torch.Tensor, num_channels: int | None = None
                         ) -> bool:
-  """Whether the library's recompute backward serves this call: 16-byte
-  aligned tensors, rows a whole number of vectors, and more than a few
-  (segment, channel) items (few items run the look-back walk, which the
-  recompute walks do not replace: those calls recompute the states with the
-  forward scan into a temporary and run the plain backward)."""
+  """Whether the recompute mode's backward runs the library's recompute
+  kernels: 16-byte aligned tensors and a geometry whose workspace buys the
+  chained walk (long segments, rows a whole number of chunks).  Other calls
+  recompute the states with the forward scan into a temporary and run the
+  plain backward: the library's per-item recompute walk is correct for any
+  geometry but, measured on ragged segments shorter than a chunk (cfg3),
+  4x slower than the forward plus the plain backward (1.70 against 0.25 +
+  0.44 ms), and few-item problems run the look-back walk."""
   if gates.data_ptr() % 16 or tokens.data_ptr() % 16:
     return False
   S, C, T = _geometry(tokens, cu, num_channels)
-  if T % (16 // tokens.element_size()):
-    return False
   lib = _lib.load()
   return lib.asc_scan_workspace_walk(
-    S, C, T, _lib.dtype_code(tokens), 1) != _lib.WALK_LOOKBACK
+    S, C, T, _lib.dtype_code(tokens), 1) == _lib.WALK_CHAINED
 
 
 def scan_bwd_recompute(grad: torch.Tensor, gates: torch.Tensor,
@@ -389,6 +390,18 @@ def scan_bwd_recompute(grad: torch.Tensor, gates: torch.Tensor,
              num_channels=num_channels)
     scan_bwd_any(grad, gates, h, d_tokens, d_gates, cu, causal, num_channels)
     return
+  scan_bwd_recompute_kernel(grad, gates, tokens, ckpt, d_tokens, d_gates, cu,
+                            causal, num_channels)
+
+
+def scan_bwd_recompute_kernel(grad: torch.Tensor, gates: torch.Tensor,
+                              tokens: torch.Tensor, ckpt: torch.Tensor,
+                              d_tokens: torch.Tensor, d_gates: torch.Tensor,
+                              cu: torch.Tensor, causal: bool,
+                              num_channels: int | None = None) -> None:
+  """asc_scan_bwd_recompute for any geometry it accepts: the chained walk
+  when the workspace buys it and every segment edge is chunk-aligned, else
+  one workgroup per (segment, channel) item."""
   lib = _lib.load()
   rs = row_constant_stride(grad, tokens, num_channels)
   if rs is None:

@@ -260,7 +260,7 @@ def main():
     log(f"[bench] parity on rows {rows}: {check}")
 
   # ---- CPU baseline on a row sample of the same inputs ----
-  cpu = None
+  cpu = cpu_ref = None
   if not a.no_cpu_baseline and with_bwd and kind == "causal" and dtype == torch.float32:
     from oracle import oracle
     threads = max(1, min(16, os.cpu_count() or 1))
@@ -282,7 +282,8 @@ def main():
     cpu_s = cpu_total / reps
     n_s = rows * Tt
     cpu = {"value": round(32 * n_s / cpu_s / 1e9, 3), "unit": "GB/s",
-           "cores": threads, "kind": "port",
+           "cores": threads, "threads": threads,
+           "host_cpus": os.cpu_count(), "kind": "port",
            "sample": f"first {rows} of {C} channels, all {B} sequences "
                      f"({n_s} elements, fwd+bwd, fp32 storage, fp64 "
                      f"accumulation, OpenMP over (sequence, channel) rows), "
@@ -290,6 +291,36 @@ def main():
                      f"{cpu_s * 1e3:.1f} ms per repetition",
            "ms_per_step_equiv": round(cpu_s * 1e3 * N / n_s, 1)}
     log(f"[bench] cpu baseline: {cpu}")
+    # the reference's own CPU method: its fp64 gold-label loop over time in
+    # torch, vectorised over the channels, and the hand-derived reverse
+    # recurrence for the backward (torch's intra-op threads)
+    L = min(4096, int(cu[1]) - int(cu[0]))
+    gs_t = g[0][:, :L].cpu()
+    xs_t = x[0][:, :L].cpu()
+    dys_t = dy[0][:, :L].cpu()
+    oracle.torch_fwd_bwd_f64(gs_t, xs_t, dys_t, [0, L])  # warm-up
+    reps, t1 = 0, time.perf_counter()
+    while True:
+      oracle.torch_fwd_bwd_f64(gs_t, xs_t, dys_t, [0, L])
+      reps += 1
+      tt = time.perf_counter() - t1
+      if tt >= 10.0 or reps >= 1000:
+        break
+    ts = tt / reps
+    n_t = C * L
+    cpu_ref = {"value": round(32 * n_t / ts / 1e9, 3), "unit": "GB/s",
+               "cores": torch.get_num_threads(),
+               "threads": torch.get_num_threads(),
+               "host_cpus": os.cpu_count(), "kind": "port",
+               "method": "the reference's CPU scan (torch fp64 loop over time, "
+                         "tests/test_scan_dtypes.py:26-38) and its reverse-"
+                         "recurrence backward (test_scan_kernels.py:873-897)",
+               "sample": f"all {C} channels x the first {L} steps of the "
+                         f"first sequence ({n_t} elements, fwd+bwd), repeated "
+                         f"{reps} times in {tt:.1f} s; {ts * 1e3:.1f} ms per "
+                         "repetition",
+               "ms_per_step_equiv": round(ts * 1e3 * N / n_t, 1)}
+    log(f"[bench] cpu baseline (reference method): {cpu_ref}")
 
   # ---- API level: the public autograd function, loss = out.sum() ----
   # (the reference's API benchmark pattern; includes the autograd
@@ -336,9 +367,9 @@ def main():
   # the default mode, with the memory each keeps between the forward and the
   # backward and the peak over the step (above what was allocated before) ----
   recompute = None
-  if (with_bwd and kind == "causal" and not a.no_recompute
-      and _ops.recompute_in_kernel(g[0], x[0], cu)):
+  if with_bwd and kind == "causal" and not a.no_recompute:
     import associative_scan_triton as ast
+    in_kernel = _ops.recompute_in_kernel(g[0], x[0], cu)
 
     def fwd_rc():
       _ops.scan_fwd(g[0], x[0], h[0], cu, reverse=False)
@@ -347,8 +378,8 @@ def main():
     ck = fwd_rc()
 
     def bwd_rc():
-      _ops.scan_bwd_recompute(dy[0], g[0], x[0], ck, dx[0], dg[0], cu,
-                              causal=True)
+      _ops.scan_bwd_recompute(dy[0], g[0], x[0], ck if in_kernel else None,
+                              dx[0], dg[0], cu, causal=True)
 
     for _ in range(a.warmup):
       fwd_rc()
@@ -405,6 +436,9 @@ def main():
     recompute = {
       "what": "backward from (dy, g, x) + per-chunk checkpoints instead of "
               "(dy, g, h): scan_causal(..., recompute_states=True)",
+      "backward": ("recompute kernels (chained walk)" if in_kernel else
+                   "states recomputed by the forward scan into a temporary, "
+                   "then the plain backward"),
       "kernel_fwd_ms": round(rf, 4), "kernel_bwd_ms": round(rb, 4),
       "kernel_fwd_bwd_ms": round(rf + rb, 4),
       "kernel_bwd_GBs": round(bwd_bytes / (rb * 1e-3) / 1e9, 2),
@@ -430,10 +464,21 @@ def main():
     del gl, xl
     log(f"[bench] recompute mode: {recompute}")
 
-  traffic = None
+  # HBM bytes per launch of the dominant kernel from a recorded rocprofv3
+  # FETCH_SIZE / WRITE_SIZE profile of this configuration (counters cannot
+  # be read from inside the run; the file names the kernel and its copy
+  # calibration); null when no profile of this configuration is recorded
+  traffic = traffic_src = None
   tf = ROOT / "profiles" / f"traffic_{a.config}.json"
   if tf.exists():
-    traffic = json.loads(tf.read_text()).get(dom)
+    import hashlib
+    rec = json.loads(tf.read_text())
+    traffic = rec.get(dom)
+    if traffic is not None:
+      traffic_src = {"file": f"profiles/{tf.name}",
+                     "sha256": hashlib.sha256(tf.read_bytes()).hexdigest()[:16],
+                     "kernel": rec.get("kernels", {}).get(dom),
+                     "recorded": True}
 
   out = {
     "metric": METRIC,
@@ -459,8 +504,10 @@ def main():
                  "peak": PEAK_HBM_GBS, "unit": "GB/s",
                  "frac": round(achieved / PEAK_HBM_GBS, 4),
                  "traffic": traffic,
+                 "traffic_source": traffic_src,
                  "algorithmic_bytes": dom_bytes},
     "cpu_baseline": cpu,
+    "cpu_baseline_reference_method": cpu_ref,
     "api": api,
     "recompute": recompute,
     "check": check,

@@ -210,5 +210,38 @@ def np_shift_pad(data, cu, pad, backward=True, wrap=True):
   return out
 
 
+# ---------------------------------------------------------------------------
+# the reference's own CPU method, in torch (timed as a CPU baseline)
+# ---------------------------------------------------------------------------
+
+def torch_fwd_bwd_f64(g, x, dy, cu):
+  """Forward and backward in torch fp64, a loop over time vectorised over
+  the channels: the forward is the reference's gold label
+  (tests/test_scan_dtypes.py:26-38, bench/bench_accuracy.py:40-49), the
+  backward its hand-derived reverse recurrence
+  (tests/test_scan_kernels.py:873-897).  Takes and returns [C, T] torch
+  tensors (h, dx, dg), per segment of cu."""
+  import torch
+  g = torch.as_tensor(g).to(torch.float64)
+  x = torch.as_tensor(x).to(torch.float64)
+  dy = torch.as_tensor(dy).to(torch.float64)
+  h = torch.zeros_like(x)
+  dx = torch.zeros_like(x)
+  dg = torch.zeros_like(x)
+  cu = [int(v) for v in cu]
+  for s in range(len(cu) - 1):
+    b, e = cu[s], cu[s + 1]
+    if e <= b:
+      continue
+    h[:, b] = x[:, b]
+    for t in range(b + 1, e):
+      h[:, t] = g[:, t] * h[:, t - 1] + x[:, t]
+    dx[:, e - 1] = dy[:, e - 1]
+    for t in range(e - 2, b - 1, -1):
+      dx[:, t] = dy[:, t] + dx[:, t + 1] * g[:, t + 1]
+    dg[:, b + 1:e] = h[:, b:e - 1] * dx[:, b + 1:e]
+  return h, dx, dg
+
+
 def default_threads() -> int:
   return max(1, min(os.cpu_count() or 1, 16))

@@ -345,3 +345,22 @@ def test_fwd_bwd_f32io_is_the_oracle_rounded(threads):
     assert np.array_equal(dg, dg64.astype(np.float32))
   # a dropped gate term in the backward would not go unnoticed
   assert not np.array_equal(dx, dy)
+
+
+def test_torch_method_is_the_oracle_bitwise():
+  """torch_fwd_bwd_f64 (the reference's CPU method, timed by bench.py as a
+  baseline) gives the C oracle's fp64 results bit for bit: both round each
+  multiply and add separately."""
+  rng = np.random.default_rng(11)
+  lens = [1, 40, 0, 300, 2]
+  cu = np.concatenate([[0], np.cumsum(lens)])
+  C, T = 5, int(cu[-1])
+  g = rng.uniform(0.5, 1.0, (C, T))
+  x = rng.standard_normal((C, T))
+  dy = rng.standard_normal((C, T))
+  h, dx, dg = (t.numpy() for t in oracle.torch_fwd_bwd_f64(g, x, dy, cu))
+  h_ref = oracle.scan_fwd(g, x, cu)
+  dx_ref, dg_ref = oracle.scan_bwd(dy, g, h_ref, cu)
+  assert np.array_equal(h, h_ref)
+  assert np.array_equal(dx, dx_ref)
+  assert np.array_equal(dg, dg_ref)

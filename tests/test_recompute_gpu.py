@@ -95,7 +95,6 @@ def _run_case(name, causal, grad_kind, spin=None, inplace=False):
   h = torch.empty_like(xd)
   _ops.scan_fwd(gd, xd, h, cu, reverse=not causal)
   ck = _ops.scan_checkpoints(h, cu, reverse=not causal)
-  assert _ops.recompute_in_kernel(gd, xd, cu)
   dx, dg = torch.empty_like(xd), torch.empty_like(xd)
   if inplace:
     dyd = dyd.contiguous()
@@ -104,7 +103,7 @@ def _run_case(name, causal, grad_kind, spin=None, inplace=False):
   _ops.USE_WORKSPACE = use_ws
   prev = lib.asc_set_lookback_spin_limit(spin) if spin is not None else None
   try:
-    _ops.scan_bwd_recompute(dyd, gd, xd, ck, dx, dg, cu, causal)
+    _ops.scan_bwd_recompute_kernel(dyd, gd, xd, ck, dx, dg, cu, causal)
     torch.cuda.synchronize()
   finally:
     _ops.USE_WORKSPACE = prev_ws
