@@ -17,7 +17,7 @@ from associative_scan_triton._build import LIB_PATH
 
 ASC_F32, ASC_F16, ASC_BF16 = 0, 1, 2
 ASC_CU_I32, ASC_CU_I64 = 0, 1
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _DTYPES = {
   torch.float32: ASC_F32,
@@ -50,6 +50,7 @@ SIGNATURES = {
   "asc_scan_bidi_bwd": [_P] * 11 + [_I, _L, _L, _L, _I, _P, _L, _P],
   "asc_scan_bidi_bwd_rowgrad": [_P, _L, _P, _L] + [_P] * 9 + [_I, _L, _L, _L, _I, _P, _L, _P],
   "asc_shift_pad": [_P, _P, _P, _I, _L, _L, _L, _I, _D, _I, _I, _P],
+  "asc_shift_pad_strided": [_P, _L, _L, _P, _L, _L, _P, _I, _L, _L, _L, _I, _D, _I, _I, _P],
 }
 # walks a workspace buys (asc_scan_workspace_walk)
 WALK_LOOKBACK = 1

@@ -433,18 +433,23 @@ def scan_bwd_recompute_kernel(grad: torch.Tensor, gates: torch.Tensor,
 
 def shift_pad(data: torch.Tensor, out: torch.Tensor, cu: torch.Tensor,
               pad_value: float, backward: bool, wrap: bool) -> None:
-  """out <- segment-aware shift of a contiguous [C, L] tensor."""
+  """out <- segment-aware shift of a [C, L] tensor; data and out may have
+  any (non-negative) strides, out must not overlap itself or data."""
   lib = _lib.load()
   dev = _lib.require_device(data, out, cu)
   if data.dim() != 2:
     raise ValueError(f"shift_pad expects a [C, BL] tensor, got {tuple(data.shape)}")
-  _check_same(data, out)
+  if out.shape != data.shape:
+    raise ValueError(f"size mismatch: {tuple(data.shape)} vs {tuple(out.shape)}")
+  if out.dtype != data.dtype:
+    raise TypeError(f"dtype mismatch: {data.dtype} vs {out.dtype}")
   dt = _lib.dtype_code(data)
   cuc = _lib.cu_code(cu)
   cu = cu.contiguous()
   C, L = data.shape
   with _OnDevice(dev):
-    _lib.check(lib.asc_shift_pad(
-      data.data_ptr(), out.data_ptr(), cu.data_ptr(), cuc, cu.numel() - 1,
+    _lib.check(lib.asc_shift_pad_strided(
+      data.data_ptr(), data.stride(0), data.stride(1), out.data_ptr(),
+      out.stride(0), out.stride(1), cu.data_ptr(), cuc, cu.numel() - 1,
       C, L, dt, float(pad_value), 1 if backward else 0, 1 if wrap else 0,
       _lib.stream_of(dev)))

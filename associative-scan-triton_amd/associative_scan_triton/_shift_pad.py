@@ -1,7 +1,8 @@
 """Segment-aware shift-and-pad (reference: _shift_pad.py:18-165).
 
 ``shift_pad`` (eager) and ``shift_pad_compiled`` (custom op
-``associative_scan_triton::shift_pad``) both run the same gfx950 kernel.
+``associative_scan_triton::shift_pad``) both run the same gfx950 kernels,
+which read the input through its strides (no copy).
 The eager form keeps the reference's zero-length check, with its exact
 message, and its torch.roll wrap-around at the row ends; the compiled form,
 like the reference's Triton kernel, clamps at the row ends and does no
@@ -37,7 +38,8 @@ def shift_pad(
   assert not (
     cu_seqlens[1:] == cu_seqlens[:-1]
   ).any(), "can't shift_pad zero-length seqments"
-  data = data.contiguous()
+  # any input strides are read in place; the result is contiguous, as
+  # torch.roll's is in the reference
   out = torch.empty_like(data, memory_format=torch.contiguous_format)
   _ops.shift_pad(data, out, cu_seqlens, pad_value, backward, wrap=True)
   return out
@@ -59,12 +61,14 @@ def shift_pad_compiled(
       backward: True = shift right (pad at seq starts),
         False = shift left (pad at seq ends)
   """
-  data = data.contiguous()
-  out = torch.empty_like(data, memory_format=torch.contiguous_format)
+  # the reference's kernel reads data through its strides and writes
+  # torch.empty_like(data), which keeps the layout of a dense input
+  # (_shift_pad.py:140,156-157); so here, with no copy of the input
+  out = torch.empty_like(data)
   _ops.shift_pad(data, out, cu_seqlens, pad_value, backward, wrap=False)
   return out
 
 
 @shift_pad_compiled.register_fake
 def _(data, cu_seqlens, pad_value, backward):
-  return torch.empty_like(data, memory_format=torch.contiguous_format)
+  return torch.empty_like(data)

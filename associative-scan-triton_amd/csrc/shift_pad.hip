@@ -9,9 +9,11 @@ namespace asc {
 namespace {
 
 // ---------------------------------------------------------------------------
-// shift_pad: elementwise, lanes interleaved (element t0 + 64*j + lane) so
-// every load/store instruction is one contiguous run.  Boundaries of the
-// wave's range are found by a binary search over cu_seqlens.
+// shift_pad: elementwise, for any strides of data and out (element (c, t) at
+// c * row_stride + t * col_stride), lanes interleaved (element t0 + 64*j +
+// lane) so that with unit column strides every load/store instruction is
+// one contiguous run.  Values move as raw bits.  Boundaries of the wave's
+// range are found by a binary search over cu_seqlens.
 // ---------------------------------------------------------------------------
 constexpr int kShiftPerLane = 8;
 constexpr int64_t kShiftChunk = kWave * kShiftPerLane;
@@ -22,11 +24,26 @@ struct ShiftParams {
   const void* cu;
   int cu64;
   int64_t S, C, L;
-  int64_t chunks;  // chunks per row
-  float pad;
+  int64_t ds0, ds1;  // data strides (elements): row, column
+  int64_t os0, os1;  // out strides
+  int64_t chunks;    // chunks per row
+  float pad;         // rounded to the element type on the device
   int backward;
   int wrap;
 };
+
+template <class IO>
+__device__ inline uint32_t raw_ld(const char* p) {
+  if (IO::ES == 4) return *reinterpret_cast<const uint32_t*>(p);
+  return *reinterpret_cast<const unsigned short*>(p);
+}
+template <class IO>
+__device__ inline void raw_st(char* p, uint32_t v) {
+  if (IO::ES == 4)
+    *reinterpret_cast<uint32_t*>(p) = v;
+  else
+    *reinterpret_cast<unsigned short*>(p) = static_cast<unsigned short>(v);
+}
 
 __device__ inline int64_t shift_boundary(const ShiftParams& p, int64_t k) {
   // k-th boundary position (k in [0, S)), ascending for a monotone cu.
@@ -47,18 +64,19 @@ __global__ void __launch_bounds__(4 * kWave) k_shift_pad(ShiftParams p) {
     const int64_t c = w / p.chunks;
     const int64_t t0 = (w - c * p.chunks) * kShiftChunk;
     const int64_t t1 = t0 + kShiftChunk < p.L ? t0 + kShiftChunk : p.L;
-    const char* row = p.data + c * p.L * IO::ES;
-    char* orow = p.out + c * p.L * IO::ES;
-    float v[kShiftPerLane];
+    const char* row = p.data + c * p.ds0 * IO::ES;
+    char* orow = p.out + c * p.os0 * IO::ES;
+    const uint32_t padb = IO::bits(p.pad);
+    uint32_t v[kShiftPerLane];
 #pragma unroll
     for (int j = 0; j < kShiftPerLane; ++j) {
       const int64_t t = t0 + j * kWave + lane;
-      v[j] = 0.0f;
+      v[j] = 0u;
       if (t < t1) {
         int64_t src = p.backward ? t - 1 : t + 1;
         if (src < 0) src = p.wrap ? p.L - 1 : 0;
         if (src >= p.L) src = p.wrap ? 0 : p.L - 1;
-        v[j] = IO::load1(row + src * IO::ES);
+        v[j] = raw_ld<IO>(row + src * p.ds1 * IO::ES);
       }
     }
     // first boundary >= t0
@@ -77,7 +95,7 @@ __global__ void __launch_bounds__(4 * kWave) k_shift_pad(ShiftParams p) {
       if (lane == static_cast<int>(off % kWave)) {
 #pragma unroll
         for (int jj = 0; jj < kShiftPerLane; ++jj)
-          if (jj == j) v[jj] = p.pad;
+          if (jj == j) v[jj] = padb;
       }
     };
     for (int64_t k = lo; k < p.S; ++k) {
@@ -95,7 +113,7 @@ __global__ void __launch_bounds__(4 * kWave) k_shift_pad(ShiftParams p) {
 #pragma unroll
     for (int j = 0; j < kShiftPerLane; ++j) {
       const int64_t t = t0 + j * kWave + lane;
-      if (t < t1) IO::store1(orow + t * IO::ES, v[j]);
+      if (t < t1) raw_st<IO>(orow + t * p.os1 * IO::ES, v[j]);
     }
   }
 }
@@ -250,8 +268,14 @@ __global__ void __launch_bounds__(4 * kWave) k_shift_pad_vec(ShiftVecParams p) {
     }
     // pad positions: first boundary >= t_lo, then every one below t_hi
     const uint32_t pad_bits = IO::bits(p.pad);
-    const ShiftParams bp{nullptr, nullptr, p.cu, p.cu64, p.S, p.C, p.L, 0, 0.0f,
-                         p.backward, p.wrap};
+    ShiftParams bp{};
+    bp.cu = p.cu;
+    bp.cu64 = p.cu64;
+    bp.S = p.S;
+    bp.C = p.C;
+    bp.L = p.L;
+    bp.backward = p.backward;
+    bp.wrap = p.wrap;
     int64_t lo = 0, hi = p.S;
     while (lo < hi) {
       const int64_t mid = (lo + hi) / 2;
@@ -297,10 +321,13 @@ using namespace asc;
 #pragma GCC visibility push(default)
 extern "C" {
 
-int asc_shift_pad(const void* data, void* out, const void* cu_seqlens,
-                  int cu_dtype, int64_t num_seq, int64_t num_channels,
-                  int64_t seq_len, int dtype, double pad_value, int backward,
-                  int wrap, void* stream) {
+int asc_shift_pad_strided(const void* data, int64_t data_row_stride,
+                          int64_t data_col_stride, void* out,
+                          int64_t out_row_stride, int64_t out_col_stride,
+                          const void* cu_seqlens, int cu_dtype, int64_t num_seq,
+                          int64_t num_channels, int64_t seq_len, int dtype,
+                          double pad_value, int backward, int wrap,
+                          void* stream) {
   int st = check_geometry(cu_seqlens, cu_dtype, num_seq, num_channels,
                           seq_len, dtype);
   if (st) return st;
@@ -308,21 +335,42 @@ int asc_shift_pad(const void* data, void* out, const void* cu_seqlens,
   const int es = elem_size(dtype);
   const void* all[2] = {data, out};
   if ((st = check_ptrs(all, 2, es))) return st;
-  if (num_channels == 0 || seq_len == 0) return ASC_OK;
+  const int64_t C = num_channels, L = seq_len;
+  if (data_row_stride < 0 || data_col_stride < 0 || out_row_stride < 0 ||
+      out_col_stride < 0)
+    return ASC_E_ARG;
+  if (C == 0 || L == 0) return ASC_OK;
+  // out must not overlap itself (each element its own address) ...
+  const int64_t a0 = C > 1 ? out_row_stride : 0, a1 = L > 1 ? out_col_stride : 0;
+  const int64_t lo = a0 < a1 ? a0 : a1, hi = a0 < a1 ? a1 : a0;
+  const int64_t lo_n = a0 < a1 ? C : L;
+  if ((C > 1 && out_row_stride == 0) || (L > 1 && out_col_stride == 0) ||
+      (lo > 0 && hi < lo * lo_n))
+    return ASC_E_ARG;
+  // ... nor the data (the shift is not done in place)
+  const int64_t dspan = ((C - 1) * data_row_stride + (L - 1) * data_col_stride + 1) * es;
+  const int64_t ospan = ((C - 1) * out_row_stride + (L - 1) * out_col_stride + 1) * es;
+  if (overlap(data, dspan, out, ospan) != kDisjoint) return ASC_E_ARG;
   ShiftParams p{};
   p.data = static_cast<const char*>(data);
   p.out = static_cast<char*>(out);
   p.cu = cu_seqlens;
   p.cu64 = cu_dtype == ASC_CU_I64;
   p.S = num_seq;
-  p.C = num_channels;
-  p.L = seq_len;
-  p.chunks = (seq_len + kShiftChunk - 1) / kShiftChunk;
+  p.C = C;
+  p.L = L;
+  p.ds0 = data_row_stride;
+  p.ds1 = data_col_stride;
+  p.os0 = out_row_stride;
+  p.os1 = out_col_stride;
+  p.chunks = (L + kShiftChunk - 1) / kShiftChunk;
   p.pad = static_cast<float>(pad_value);
   p.backward = backward ? 1 : 0;
   p.wrap = wrap ? 1 : 0;
   const int v = 16 / es;
-  const int ph = common_phase(all, 2, es, v);
+  const bool dense = data_col_stride == 1 && out_col_stride == 1 &&
+                     (C == 1 || (data_row_stride == L && out_row_stride == L));
+  const int ph = dense ? common_phase(all, 2, es, v) : -1;
   if (ph >= 0) {
     ShiftVecParams q{};
     q.data = p.data - static_cast<int64_t>(ph) * es;
@@ -354,6 +402,15 @@ int asc_shift_pad(const void* data, void* out, const void* cu_seqlens,
     default: fn = reinterpret_cast<const void*>(&k_shift_pad<IoBF16>); break;
   }
   return launch(fn, (p.C * p.chunks + 3) / 4, 4, p, stream);
+}
+
+int asc_shift_pad(const void* data, void* out, const void* cu_seqlens,
+                  int cu_dtype, int64_t num_seq, int64_t num_channels,
+                  int64_t seq_len, int dtype, double pad_value, int backward,
+                  int wrap, void* stream) {
+  return asc_shift_pad_strided(data, seq_len, 1, out, seq_len, 1, cu_seqlens,
+                               cu_dtype, num_seq, num_channels, seq_len, dtype,
+                               pad_value, backward, wrap, stream);
 }
 
 }  // extern "C"

@@ -67,7 +67,7 @@ enum {
 };
 
 /* ABI version of this header; bumped on any signature change. */
-#define ASC_ABI_VERSION 5
+#define ASC_ABI_VERSION 6
 int asc_abi_version(void);
 
 /*
@@ -330,6 +330,24 @@ int asc_shift_pad(const void* data, void* out, const void* cu_seqlens,
                   int cu_dtype, int64_t num_seq, int64_t num_channels,
                   int64_t seq_len, int dtype, double pad_value, int backward,
                   int wrap, void* stream);
+
+/*
+ * asc_shift_pad for any element strides: element (c, p) of data lives at
+ * data + (c * data_row_stride + p * data_col_stride) elements, and likewise
+ * for out (a transposed or sliced view needs no copy).  Strides are >= 0;
+ * out must not overlap itself or data (ASC_E_ARG).  Values move as raw bits.
+ * asc_shift_pad is this call with contiguous rows (strides seq_len, 1).
+ *
+ * Replaces: _shift_pad.py:140-157, whose kernel takes data.stride(0) and
+ *   data.stride(1) and writes torch.empty_like(data).
+ */
+int asc_shift_pad_strided(const void* data, int64_t data_row_stride,
+                          int64_t data_col_stride, void* out,
+                          int64_t out_row_stride, int64_t out_col_stride,
+                          const void* cu_seqlens, int cu_dtype, int64_t num_seq,
+                          int64_t num_channels, int64_t seq_len, int dtype,
+                          double pad_value, int backward, int wrap,
+                          void* stream);
 
 #ifdef __cplusplus
 }

@@ -39,7 +39,7 @@ def test_exports_every_declared_symbol():
 
 def test_abi_version_and_strerror():
   lib = _lib.load()
-  assert lib.asc_abi_version() == 5
+  assert lib.asc_abi_version() == 6
   assert lib.asc_strerror(0) == b"success"
   for code in (-1, -2, -3, -4, -5, -6):
     assert lib.asc_strerror(code) and lib.asc_strerror(code) != b"unknown error"
@@ -248,3 +248,21 @@ def test_recompute_entry_points_validation():
   assert lib.asc_scan_checkpoints(64, 66, 8, 0, 0, 1, 4, 0, 0, None) == -4
   assert lib.asc_scan_checkpoints(64, 72, 8, 0, 0, 1, 4, 0, 0, None) == -5
   assert lib.asc_scan_checkpoints(None, 128, 8, 0, 0, 1, 4, 0, 0, None) == -1
+
+
+def test_shift_pad_strided_validation():
+  """Strides are >= 0; out must not overlap itself or data (host checks,
+  before any launch); C = 0 launches nothing."""
+  lib = _lib.load()
+
+  def sp(data=64, ds0=4, ds1=1, out=256, os0=4, os1=1, C=0, L=4):
+    return lib.asc_shift_pad_strided(data, ds0, ds1, out, os0, os1, 8, 0, 1,
+                                     C, L, 0, 0.0, 1, 1, None)
+
+  assert sp() == 0
+  assert sp(C=2, ds0=-1) == -5
+  assert sp(C=2, os0=2) == -5            # rows of out overlap
+  assert sp(C=2, os0=0) == -5
+  assert sp(C=2, out=64) == -5           # in place
+  assert sp(C=2, out=72) == -5           # overlapping data
+  assert sp(C=2, data=None) == -1

@@ -18,6 +18,7 @@ tests/test_scan_causal.py:52-71 (out.sum() losses), _dispatcher.py:35-37
 and _kernels.py:77-81 (in-place writes).
 """
 
+import numpy as np
 import pytest
 import torch
 
@@ -267,3 +268,56 @@ def test_deterministic_mode_repeats_bitwise(dtype):
   dx_ref, dg_ref = oracle_bwd(dy, g, npf(y), lens)
   check_close(dx, dx_ref, dtype, "dx")
   check_close(dg, dg_ref, dtype, "dg")
+
+
+# ---------------------------------------------------------------------------
+# shift_pad on strided inputs (no copy; _shift_pad.py:140,156-157)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
+                         ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("layout", ["transposed", "sliced", "row-broadcast"])
+@pytest.mark.parametrize("backward", [True, False])
+def test_shift_pad_strided_inputs(dtype, layout, backward):
+  """Transposed, column-sliced and row-broadcast views are read through
+  their strides: the compiled form writes torch.empty_like(data) (the
+  transposed layout is kept), the eager form a contiguous tensor.  A shift
+  only moves bits, so the oracle runs on the raw bit patterns (integers,
+  exact in fp64, a NaN payload included) and both results must match them
+  bit for bit."""
+  from oracle import oracle
+  C, L = 37, 1000
+  lens = [1, 300, 7, 692]
+  cu = torch.tensor(cu_of(lens), device=DEV, dtype=torch.int32)
+  gen = torch.Generator().manual_seed(8)
+  if layout == "transposed":
+    base = torch.randn(L, C, generator=gen).to(dtype)
+    base[17, 2] = float("nan")
+    data = base.to(DEV).t()
+  elif layout == "sliced":
+    base = torch.randn(C, L + 13, generator=gen).to(dtype)
+    base[2, 5 + 17] = float("nan")
+    data = base.to(DEV)[:, 5:5 + L]
+  else:
+    base = torch.randn(1, L, generator=gen).to(dtype)
+    data = base.to(DEV).expand(C, L)
+  iv = torch.int32 if dtype == torch.float32 else torch.int16
+  if dtype != torch.float32 and layout != "row-broadcast":
+    # a NaN with a payload (quiet bit plus low bits)
+    nan_bits = torch.tensor([0x7FC5 if dtype == torch.bfloat16 else 0x7E05],
+                            dtype=torch.int16).view(dtype)
+    data[2, 17] = nan_bits.to(DEV)[0]
+  src = data.cpu().contiguous().view(iv).to(torch.int64).numpy().astype(float)
+  pad = float(torch.tensor([0.5], dtype=dtype).view(iv).item())
+  cu_np = cu_of(lens)
+  for compiled, out in ((True, ast.shift_pad_compiled(data, cu, 0.5, backward)),
+                        (False, ast.shift_pad(data, cu, 0.5, backward))):
+    exp = oracle.shift_pad(src, cu_np, pad, backward=backward,
+                           wrap=not compiled)
+    got = out.cpu().contiguous().view(iv).to(torch.int64).numpy()
+    assert out.shape == (C, L)
+    assert (got == exp.astype(np.int64)).all(), (compiled, layout)
+    if compiled and layout == "transposed":
+      assert out.stride() == data.stride()
+    if not compiled:
+      assert out.is_contiguous()
