@@ -12,33 +12,46 @@ import torch
 
 from associative_scan_triton import _lib
 
-# Problems with few (segment, channel) items run the library's look-back walk,
-# and long chunk-aligned segments its chained walk; both need a workspace,
-# and the library says how large (0 = none needed).  False forces the
+# Problems with few (segment, channel) items run the library's tree walk (or
+# its look-back walk when the tensors do not share one 16-byte phase), and
+# long chunk-aligned segments its chained walk; all need a workspace, and
+# the library says how large (0 = none needed).  False forces the
 # workspace-free walks (the walks agree to fp32 rounding).
 USE_WORKSPACE = True
 
 
-def _walk(lib, S: int, C: int, T: int, dtype_code: int, nbranch: int) -> int:
+def _one_phase(tensors) -> bool:
+  """Whether the tensors' addresses agree modulo 16 bytes (the library then
+  takes the tree walk, not the look-back walk, for few items)."""
+  return bool(tensors) and len({t.data_ptr() % 16 for t in tensors}) == 1
+
+
+def _walk(lib, S: int, C: int, T: int, dtype_code: int, nbranch: int,
+          tensors=()) -> int:
   """The walk a workspace would buy for this geometry (0: none is used).
 
-  The look-back walk's last bits can vary from run to run (which
-  predecessor a tile meets as inclusive depends on timing); under
-  torch.use_deterministic_algorithms(True) it is not used, and the
-  workspace-free walks, which are bitwise reproducible, run instead."""
+  For few items the library runs the tree walk, whose results repeat bit
+  for bit, when every tensor of the call (`tensors`) has the same address
+  modulo 16 bytes, and otherwise the look-back walk, whose last bits can
+  vary from run to run (which predecessor a tile meets as inclusive depends
+  on timing); under torch.use_deterministic_algorithms(True) the latter is
+  not used, and the workspace-free walks, which are bitwise reproducible,
+  run instead."""
   if not USE_WORKSPACE:
     return 0
   walk = lib.asc_scan_workspace_walk(S, C, T, dtype_code, nbranch)
-  if walk == _lib.WALK_LOOKBACK and torch.are_deterministic_algorithms_enabled():
+  if (walk == _lib.WALK_LOOKBACK and torch.are_deterministic_algorithms_enabled()
+      and not _one_phase(tensors)):
     return 0
   return max(walk, 0)
 
 
 def _workspace(lib, dev: torch.device, S: int, C: int, T: int,
-               dtype_code: int, nbranch: int):
+               dtype_code: int, nbranch: int, *tensors):
   """A workspace from torch's caching allocator when the geometry wants one
-  (the library clears it on the launch stream), else (None, 0)."""
-  if not _walk(lib, S, C, T, dtype_code, nbranch):
+  (the library clears it on the launch stream), else (None, 0); `tensors`
+  are the call's tensors (see _walk)."""
+  if not _walk(lib, S, C, T, dtype_code, nbranch, tensors):
     return None, 0
   nbytes = lib.asc_scan_workspace_bytes(S, C, T, dtype_code, nbranch)
   if nbytes <= 0:
@@ -119,7 +132,8 @@ def scan_fwd(gates: torch.Tensor, tokens: torch.Tensor, h_out: torch.Tensor,
   with _OnDevice(dev):
     # the gate product and in-place calls run the workspace-free walks
     plain = gate_prod_out is None and h_out.data_ptr() != tokens.data_ptr()
-    ws, nb = _workspace(lib, dev, S, C, T, dt, 1) if plain else (None, 0)
+    ws, nb = (_workspace(lib, dev, S, C, T, dt, 1, gates, tokens, h_out)
+              if plain else (None, 0))
     _lib.check(lib.asc_scan_fwd(
       gates.data_ptr(), tokens.data_ptr(), h_out.data_ptr(),
       _lib.ptr(gate_prod_out), cu.data_ptr(), cuc, S, C, T, dt,
@@ -140,7 +154,8 @@ def scan_bwd(grad: torch.Tensor, gates: torch.Tensor, states: torch.Tensor,
   with _OnDevice(dev):
     # d_tokens in place of the gradient runs the workspace-free walks
     plain = d_tokens.data_ptr() != grad.data_ptr()
-    ws, nb = _workspace(lib, dev, S, C, T, dt, 1) if plain else (None, 0)
+    ws, nb = (_workspace(lib, dev, S, C, T, dt, 1, grad, gates, states,
+                         d_tokens, d_gates) if plain else (None, 0))
     _lib.check(lib.asc_scan_bwd(
       grad.data_ptr(), gates.data_ptr(), states.data_ptr(),
       d_tokens.data_ptr(), d_gates.data_ptr(), cu.data_ptr(), cuc, S, C, T,
@@ -183,7 +198,8 @@ def scan_bwd_rowgrad(grad: torch.Tensor, row_stride: int, gates: torch.Tensor,
   cu = cu.contiguous()
   S, C, T = _geometry(states, cu, num_channels)
   with _OnDevice(dev):
-    ws, nb = _workspace(lib, dev, S, C, T, dt, 1)
+    ws, nb = _workspace(lib, dev, S, C, T, dt, 1, gates, states, d_tokens,
+                        d_gates)
     _lib.check(lib.asc_scan_bwd_rowgrad(
       grad.data_ptr(), int(row_stride), gates.data_ptr(), states.data_ptr(),
       d_tokens.data_ptr(), d_gates.data_ptr(), cu.data_ptr(), cuc, S, C, T,
@@ -196,15 +212,16 @@ def scan_bwd_any(grad: torch.Tensor, gates: torch.Tensor, states: torch.Tensor,
                  num_channels: int | None = None) -> None:
   """Backward for any incoming gradient layout: a gradient that is constant
   along time is read one value per row (no materialised copy) unless the
-  geometry runs the look-back walk for few items, which needs the full
-  gradient; any other layout is made contiguous, as the reference does
-  (scan_eager.py:61)."""
+  geometry runs the look-back walk for few items (tensors of different
+  16-byte phases), which needs the full gradient; any other layout is made
+  contiguous, as the reference does (scan_eager.py:61)."""
   rs = row_constant_stride(grad, states, num_channels)
   if rs is not None:
     lib = _lib.load()
     cu_c = cu.contiguous()
     S, C, T = _geometry(states, cu_c, num_channels)
-    if _walk(lib, S, C, T, _lib.dtype_code(states), 1) != _lib.WALK_LOOKBACK:
+    if (_walk(lib, S, C, T, _lib.dtype_code(states), 1) != _lib.WALK_LOOKBACK
+        or _one_phase((gates, states, d_tokens, d_gates))):
       scan_bwd_rowgrad(grad, rs, gates, states, d_tokens, d_gates, cu_c,
                        causal, num_channels)
       return
@@ -224,7 +241,7 @@ def scan_bidi_fwd(gf: torch.Tensor, xf: torch.Tensor, gb: torch.Tensor,
   cu = cu.contiguous()
   S, C, T = _geometry(xf, cu, num_channels)
   with _OnDevice(dev):
-    ws, nb = _workspace(lib, dev, S, C, T, dt, 2)
+    ws, nb = _workspace(lib, dev, S, C, T, dt, 2, gf, xf, gb, xb, hf, hb)
     _lib.check(lib.asc_scan_bidi_fwd(
       gf.data_ptr(), xf.data_ptr(), gb.data_ptr(), xb.data_ptr(),
       hf.data_ptr(), hb.data_ptr(), cu.data_ptr(), cuc, S, C, T, dt,
@@ -245,7 +262,8 @@ def scan_bidi_bwd(dyf: torch.Tensor, dyb: torch.Tensor, gf: torch.Tensor,
   cu = cu.contiguous()
   S, C, T = _geometry(dyf, cu, num_channels)
   with _OnDevice(dev):
-    ws, nb = _workspace(lib, dev, S, C, T, dt, 2)
+    ws, nb = _workspace(lib, dev, S, C, T, dt, 2, dyf, dyb, gf, gb, hf, hb,
+                        dxf, dgf, dxb, dgb)
     _lib.check(lib.asc_scan_bidi_bwd(
       dyf.data_ptr(), dyb.data_ptr(), gf.data_ptr(), gb.data_ptr(),
       hf.data_ptr(), hb.data_ptr(), dxf.data_ptr(), dgf.data_ptr(),
@@ -273,7 +291,8 @@ def scan_bidi_bwd_rowgrad(dyf: torch.Tensor, rsf: int, dyb: torch.Tensor,
   cu = cu.contiguous()
   S, C, T = _geometry(hf, cu, num_channels)
   with _OnDevice(dev):
-    ws, nb = _workspace(lib, dev, S, C, T, dt, 2)
+    ws, nb = _workspace(lib, dev, S, C, T, dt, 2, gf, gb, hf, hb, dxf, dgf,
+                        dxb, dgb)
     _lib.check(lib.asc_scan_bidi_bwd_rowgrad(
       dyf.data_ptr(), int(rsf), dyb.data_ptr(), int(rsb), gf.data_ptr(),
       gb.data_ptr(), hf.data_ptr(), hb.data_ptr(), dxf.data_ptr(),
@@ -290,8 +309,8 @@ def scan_bidi_bwd_any(dyf: torch.Tensor | None, dyb: torch.Tensor | None,
   for a branch whose output received no gradient (zero).  When both
   gradients are constant along time (stride-0 expanded tensors, or None)
   they are read one value per row, unless the geometry runs the look-back
-  walk for few items; otherwise both are made contiguous, as the reference does
-  (scan_eager.py:161,166)."""
+  walk for few items (tensors of different 16-byte phases); otherwise both
+  are made contiguous, as the reference does (scan_eager.py:161,166)."""
   zero = None
   if dyf is None or dyb is None:
     zero = torch.zeros((), dtype=hf.dtype, device=hf.device)
@@ -301,7 +320,8 @@ def scan_bidi_bwd_any(dyf: torch.Tensor | None, dyb: torch.Tensor | None,
     lib = _lib.load()
     cu_c = cu.contiguous()
     S, C, T = _geometry(hf, cu_c, num_channels)
-    if _walk(lib, S, C, T, _lib.dtype_code(hf), 2) != _lib.WALK_LOOKBACK:
+    if (_walk(lib, S, C, T, _lib.dtype_code(hf), 2) != _lib.WALK_LOOKBACK
+        or _one_phase((gf, gb, hf, hb, dxf, dgf, dxb, dgb))):
       scan_bidi_bwd_rowgrad(zero if dyf is None else dyf, rsf,
                             zero if dyb is None else dyb, rsb, gf, gb, hf, hb,
                             dxf, dgf, dxb, dgb, cu_c, num_channels)

@@ -650,12 +650,15 @@ __device__ inline int wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
 }
 
-// skip: nullptr, or a flag in device memory that, when set, makes every
-// workgroup return at once (the chained walk ran instead; see scan_chain.hip).
+// skip: nullptr, or a flag in device memory that makes every workgroup
+// return at once when it is set (the chained walk ran instead; see
+// scan_chain.hip) or, with skip_if_clear, when it is clear (the tree walk
+// ran and no wait of it failed; see scan_tree.hip).
 struct FwdParams {
   Geometry geo;
   FwdPtrs br[2];
   const uint32_t* skip;
+  int skip_if_clear;
 };
 
 struct BwdParams {
@@ -663,11 +666,12 @@ struct BwdParams {
   BwdPtrs br[2];
   int64_t dy_rs[2];  // DYC: element stride between rows of each gradient
   const uint32_t* skip;
+  int skip_if_clear;
 };
 
 template <class Params>
 __device__ inline bool skipped(const Params& p) {
-  return p.skip != nullptr && *p.skip != 0u;
+  return p.skip != nullptr && ((*p.skip != 0u) != (p.skip_if_clear != 0));
 }
 
 // Grid of a per-item walk launched behind the chained walk (usually
@@ -832,6 +836,23 @@ bool lb_fwd(const FwdParams& p, int dtype, int dirs, bool aln, void* ws,
             int64_t ws_bytes, void* stream, int& status);
 bool lb_bwd(const BwdParams& p, int dtype, int dirs, bool aln, void* ws,
             int64_t ws_bytes, void* stream, int& status);
+
+// scan_tree.hip: the tree walk over chunks of the flat array (few items;
+// any cu_seqlens; tensors of one phase).  tree_bytes: its workspace for n
+// elements per branch (0 when it cannot run); tree_fwd returns false
+// (nothing launched) when it cannot run or the workspace is missing or too
+// small, else true with the launch status in `status` and *fail pointing
+// at a device flag that is set exactly when a bounded wait expired: the
+// caller then launches a workspace-free walk that runs only when it is set.
+int64_t tree_bytes(int64_t n, int v, int nbranch);
+bool tree_fwd(const FwdParams& p, int dtype, int dirs, bool aln, void* ws,
+              int64_t ws_bytes, void* stream, int& status,
+              const uint32_t** fail);
+// The backward, as tree_fwd (dyc: gradients constant along time, one value
+// per row at p.dy_rs).
+bool tree_bwd(const BwdParams& p, int dtype, int dirs, bool aln, bool dyc,
+              void* ws, int64_t ws_bytes, void* stream, int& status,
+              const uint32_t** fail);
 
 // scan_chain.hip: chained chunks for segments aligned to the chunk size.
 // chain_bytes: its workspace (0 when the geometry cannot use it).

@@ -18,6 +18,11 @@
 constexpr int64_t kScratchBytes = int64_t(8) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
+// Few-item problems: the tree walk (1) or the look-back walk (0).
+#ifndef ASC_USE_TREE
+#define ASC_USE_TREE 1
+#endif
+
 namespace asc {
 namespace {
 
@@ -115,7 +120,16 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
   // place; they need the caller's workspace (else the per-item walks run)
   const bool walks_ok = !wa && !inplace;
   if (walks_ok && lb_use(S, C, T, nbranch, v)) {
-    if (lb_fwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st)) return st;
+    // few items: the tree walk (deterministic), or the look-back walk for
+    // tensors of different phases
+    if (ASC_USE_TREE &&
+        tree_fwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st, &p.skip)) {
+      // the workspace-free walk below runs only if a tree wait failed
+      if (st) return st;
+      p.skip_if_clear = 1;
+    } else if (lb_fwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st)) {
+      return st;
+    }
   } else if (walks_ok && chain_fwd(p, dtype, aln, dirs, ws, ws_bytes, stream,
                                    st, &p.skip)) {
     // the per-item walk below runs only if cu_seqlens turns out unaligned
@@ -191,7 +205,15 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
     p.br[b].pend = p.geo.phase + C * T;
   }
   for (int b = 0; b < nbranch; ++b) p.dy_rs[b] = dyc ? dy_rs[b] : 0;
-  if (!inplace && !dyc && lb_use(S, C, T, nbranch, v)) {
+  // few items: the tree walk, else (tensors of different phases) the
+  // look-back walk, which takes dense gradients only
+  const bool few = !inplace && lb_use(S, C, T, nbranch, v);
+  if (few && ASC_USE_TREE &&
+      tree_bwd(p, dtype, dirs, aln, dyc, ws, ws_bytes, stream, st, &p.skip)) {
+    // the workspace-free walk below runs only if a tree wait failed
+    if (st) return st;
+    p.skip_if_clear = 1;
+  } else if (few && !dyc) {
     if (lb_bwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st)) return st;
   } else if (!inplace && chain_bwd(p, dtype, aln, dyc, dirs, ws, ws_bytes,
                                    stream, st, &p.skip)) {
@@ -259,8 +281,11 @@ int64_t asc_scan_workspace_bytes(int64_t num_seq, int64_t num_channels,
     return ASC_E_ARG;
   if (num_channels > 0 && seq_stride > (INT64_MAX / 64) / num_channels)
     return ASC_E_SIZE;
-  if (lb_use(num_seq, num_channels, seq_stride, nbranch, 16 / es))
-    return lb_bytes(num_channels * seq_stride, 16 / es, nbranch);
+  if (lb_use(num_seq, num_channels, seq_stride, nbranch, 16 / es)) {
+    const int64_t lb = lb_bytes(num_channels * seq_stride, 16 / es, nbranch);
+    const int64_t tr = tree_bytes(num_channels * seq_stride, 16 / es, nbranch);
+    return lb > tr ? lb : tr;
+  }
   return chain_bytes(num_seq, num_channels, seq_stride, 16 / es, nbranch);
 }
 

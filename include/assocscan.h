@@ -20,14 +20,18 @@
  * Workspace: the scan entry points take an optional caller-owned device
  * buffer (32-byte aligned, asc_scan_workspace_bytes() bytes).  Problems
  * with few (segment, channel) items -- one long sequence, a handful of
- * channels -- want it: with it they run a single-pass decoupled look-back
- * walk over tiles of 16384 elements that keeps every CU busy (the buffer
- * holds one 16-byte carry slot per tile and is cleared by the call itself,
- * on `stream`).  Every other problem, and any call given NULL or a buffer
- * too small, runs the workspace-free walks (one wave or one workgroup per
- * item).  Results agree to fp32 rounding; the workspace-free walks are
- * bitwise reproducible, the look-back walk's last bits can vary from run
- * to run.  Two calls that run at the same time must not share a workspace.
+ * channels -- want it: with it they run a single-pass walk over chunks of
+ * 8192 fp32 / 16384 fp16-bf16 elements that keeps every CU busy, whose
+ * carries go through a tree of 16-byte slots in the buffer (when every
+ * tensor of the call has the same address modulo 16 bytes; otherwise a
+ * decoupled look-back walk over tiles of 16384 elements, one slot per
+ * tile).  Long chunk-aligned segments use it for a chained-chunk walk (see
+ * asc_scan_workspace_walk).  The call clears what it uses on `stream`.
+ * Every other problem, and any call given NULL or a buffer too small, runs
+ * the workspace-free walks (one wave or one workgroup per item).  Results
+ * agree to fp32 rounding; every walk but the look-back walk is bitwise
+ * reproducible, the look-back walk's last bits can vary from run to run.
+ * Two calls that run at the same time must not share a workspace.
  *
  * The reference is the Triton package associative-scan-triton 1.0.0; the
  * citations below name the reference function each entry point replaces.
@@ -84,22 +88,25 @@ int64_t asc_scan_workspace_bytes(int64_t num_seq, int64_t num_channels,
 /*
  * Which walk a workspace of asc_scan_workspace_bytes() buys for this
  * geometry: 0 = none (the workspace-free walks run), ASC_WALK_LOOKBACK (few
- * items; any cu_seqlens), ASC_WALK_CHAINED (long segments; runs when every
- * edge in cu_seqlens is a multiple of the chunk size -- 4096 fp32 / 8192
- * fp16-bf16 elements -- checked on the device, else the workspace-free walks
- * run), or a negative ASC_E_* code.  The row-gradient entry points below
- * cannot use the look-back walk.  No reference counterpart.
+ * items, any cu_seqlens: the tree walk, or the look-back walk for tensors at
+ * different 16-byte phases), ASC_WALK_CHAINED (long segments; runs when
+ * every edge in cu_seqlens is a multiple of the chunk size -- 4096 fp32 /
+ * 8192 fp16-bf16 elements -- checked on the device, else the workspace-free
+ * walks run), or a negative ASC_E_* code.  The row-gradient entry points
+ * below cannot use the look-back walk (they take the workspace-free walks
+ * instead).  No reference counterpart.
  */
 enum { ASC_WALK_LOOKBACK = 1, ASC_WALK_CHAINED = 2 };
 int asc_scan_workspace_walk(int64_t num_seq, int64_t num_channels,
                             int64_t seq_stride, int dtype, int nbranch);
 
 /*
- * Test hook, no reference counterpart: sets how many times a look-back or
- * chained-walk wave polls a preceding tile's slot before it computes that
- * tile's carry map from the tile's inputs itself (0 = always compute; the
- * default keeps the fallback for pathological scheduling only).  Returns
- * the previous value.  Process-wide (an atomic: safe to call from any host
+ * Test hook, no reference counterpart: sets how many times a wave of the
+ * look-back, chained or tree walk polls a preceding tile's slot before it
+ * gives up waiting: a look-back wave then computes that tile's carry map
+ * from the tile's inputs itself; a chained or tree walk's call is redone
+ * by a workspace-free walk (0 = give up at once; the default keeps the
+ * fallback for pathological scheduling only).  Returns the previous value.  Process-wide (an atomic: safe to call from any host
  * thread); affects launches issued after the call.
  */
 unsigned asc_set_lookback_spin_limit(unsigned polls);
@@ -116,8 +123,9 @@ const char* asc_strerror(int status);
  * In-place use is allowed: h_out may equal tokens and gate_prod_out may
  * equal gates (each element is read before it is overwritten).  Such a call,
  * and any call with gate_prod_out, runs the workspace-free walks (the
- * bounded-wait fallbacks of the look-back and chained walks re-read inputs
- * of earlier tiles, which an in-place call may already have overwritten).
+ * bounded-wait fallbacks of the tree, look-back and chained walks re-read
+ * inputs of earlier tiles, which an in-place call may already have
+ * overwritten).
  * Any other overlap between an output and an input, or between the two
  * outputs, returns ASC_E_ARG.
  *
@@ -135,7 +143,7 @@ int asc_scan_fwd(const void* gates, const void* tokens, void* h_out,
 
 /*
  * asc_scan_fwd without a workspace argument and without any allocation:
- * the look-back and chained walks take their carry slots from a static
+ * the tree, look-back and chained walks take their carry slots from a static
  * device array of 8 MiB that the library holds on each GPU it runs on
  * until the process ends (looked up once per device, with hipGetSymbolAddress,
  * on the first call).  Same arguments, results and aliasing rule as
@@ -151,7 +159,7 @@ int asc_scan_fwd(const void* gates, const void* tokens, void* h_out,
  * No reference counterpart: for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc), which with asc_scan_fwd could only pass NULL and lose the
- * look-back and chained walks.
+ * tree, look-back and chained walks.
  */
 int asc_scan_fwd_noalloc(const void* gates, const void* tokens, void* h_out,
                          void* gate_prod_out, const void* cu_seqlens,
@@ -192,8 +200,9 @@ int asc_scan_bwd(const void* grad, const void* gates, const void* states,
  * PyTorch hands over as a stride-0 expanded tensor.  The kernels read one
  * value per row instead of a [C, T] tensor: 4 of the 5 tensors' traffic, and
  * no materialised copy.  The workspace is used as by asc_scan_bwd, except
- * that the look-back walk for few items does not take this form of the
- * gradient (those calls run the workspace-free walks).
+ * that the look-back walk for few items (tensors at different 16-byte
+ * phases) does not take this form of the gradient (those calls run the
+ * workspace-free walks).
  *
  * Replaces: scan_eager.py:58-63 (grad_output.contiguous() followed by
  *   backward_scan_fused_full) and scan_compiled.py:158-166 when the incoming

@@ -73,13 +73,29 @@ def test_host_validation_codes():
 
 def test_workspace_bytes():
   lib = _lib.load()
-  # few (segment, channel) items: one 16-byte slot per tile of 16384 elements
-  # (counted for the worst-case phase), per branch
+  # few (segment, channel) items: the larger of the tree walk's need (a
+  # 256-byte flag block, then per branch one 16-byte slot per chunk of
+  # 8192 fp32 / 16384 fp16-bf16 elements and one per group of 64 slots of
+  # the level below, up to a level of at most 64) and the look-back walk's
+  # (one slot per tile of 16384 elements); both for the worst-case phase
+  def tree(n, chunk, nbranch):
+    cnt, slots = -(-n // chunk), 0
+    while True:
+      slots += cnt
+      if cnt <= 64:
+        break
+      cnt = -(-cnt // 64)
+    return 256 + 16 * slots * nbranch
+
   n = 4 * 1_000_000
   b1 = lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 0, 1)
   b2 = lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 0, 2)
-  assert b1 == 16 * -(-(n + 3) // 16384) and b2 == 2 * b1
-  assert lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 2, 1) == 16 * -(-(n + 7) // 16384)
+  assert b1 == max(tree(n + 3, 8192, 1), 16 * -(-(n + 3) // 16384))
+  assert b2 == max(tree(n + 3, 8192, 2), 2 * 16 * -(-(n + 3) // 16384))
+  assert lib.asc_scan_workspace_bytes(2, 4, 1_000_000, 2, 1) == max(
+    tree(n + 7, 16384, 1), 16 * -(-(n + 7) // 16384))
+  # one row of 2^27 elements: 16385 chunks, 257 groups, 5 groups of groups
+  assert lib.asc_scan_workspace_bytes(1, 1, 1 << 27, 0, 1) == tree((1 << 27) + 3, 8192, 1)
   # many items (more than 128 (segment, channel, branch) items): rows that
   # are a whole number of chunks (4096 fp32 / 8192 fp16-bf16 elements) with
   # segments of at least one chunk on average take the chained walk, a

@@ -125,16 +125,25 @@ def test_row_constant_stride_detection():
 
 
 def test_deterministic_mode_avoids_lookback():
-  """Under torch.use_deterministic_algorithms(True) the look-back walk (its
-  last bits can vary from run to run) is not used; the chained walk, whose
-  carries are composed in a fixed order, still is."""
+  """Under torch.use_deterministic_algorithms(True) the few-item walk is
+  kept only when every tensor of the call has the same address modulo 16
+  bytes (the library then runs the tree walk, which composes carries in a
+  fixed order; otherwise the look-back walk, whose last bits can vary from
+  run to run); the chained walk, whose carries are composed in a fixed
+  order, is always kept."""
   from associative_scan_triton import _lib, _ops
   lib = _lib.load()
+  base = torch.empty(64)
+  same = (base[0:8], base[4:12], torch.empty(8))   # 0, 16, 0 mod 16 bytes
+  mixed = (base[0:8], base[1:9])                   # 0 and 4 mod 16 bytes
   assert _ops._walk(lib, 2, 4, 1_000_000, 0, 1) == _lib.WALK_LOOKBACK
+  assert _ops._walk(lib, 2, 4, 1_000_000, 0, 1, mixed) == _lib.WALK_LOOKBACK
   prev = torch.are_deterministic_algorithms_enabled()
   torch.use_deterministic_algorithms(True)
   try:
     assert _ops._walk(lib, 2, 4, 1_000_000, 0, 1) == 0
+    assert _ops._walk(lib, 2, 4, 1_000_000, 0, 1, mixed) == 0
+    assert _ops._walk(lib, 2, 4, 1_000_000, 0, 1, same) == _lib.WALK_LOOKBACK
     assert _ops._walk(lib, 8, 1536, 524288, 0, 1) == _lib.WALK_CHAINED
   finally:
     torch.use_deterministic_algorithms(prev)

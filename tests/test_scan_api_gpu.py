@@ -11,7 +11,9 @@
   in-place backward (d_tokens over the gradient) on geometries whose
   out-of-place calls take the chained or look-back walk, with the
   bounded-wait fallback at its default and forced on every poll.
-* Deterministic mode: few-item problems repeat bit for bit.
+* Few-item problems (the tree walk) repeat bit for bit, by default and in
+  deterministic mode; its bounded-wait fallback and the look-back walk (for
+  tensors of different 16-byte phases) agree with the oracle.
 
 Reference: scan_eager.py:50-64 (backward of grad_output.contiguous()),
 tests/test_scan_causal.py:52-71 (out.sum() losses), _dispatcher.py:35-37
@@ -236,11 +238,13 @@ def test_overlapping_outputs_are_refused():
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
-def test_deterministic_mode_repeats_bitwise(dtype):
-  """torch.use_deterministic_algorithms(True): a few-item geometry (whose
-  default walk is the look-back walk) runs the workspace-free walks, and
-  repeated forward + backward calls through the autograd API give identical
-  bits, within tolerance of the oracle."""
+@pytest.mark.parametrize("mode", ["default", "deterministic"])
+def test_few_items_repeat_bitwise(dtype, mode):
+  """A few-item geometry (the tree walk: carries composed in an order fixed
+  by the data) gives identical bits on repeated forward + backward calls
+  through the autograd API, by default and under
+  torch.use_deterministic_algorithms(True), within tolerance of the
+  oracle."""
   lens, C = [300001, 70000, 5], 2
   T = sum(lens)
   lib = _lib.load()
@@ -249,7 +253,7 @@ def test_deterministic_mode_repeats_bitwise(dtype):
   g, x, dy = make(lens, C, dtype, glo=0.5, n=3)
   args = grid_args(lens, C)
   prev = torch.are_deterministic_algorithms_enabled()
-  torch.use_deterministic_algorithms(True)
+  torch.use_deterministic_algorithms(mode == "deterministic")
   try:
     runs = []
     for _ in range(3):
@@ -268,6 +272,52 @@ def test_deterministic_mode_repeats_bitwise(dtype):
   dx_ref, dg_ref = oracle_bwd(dy, g, npf(y), lens)
   check_close(dx, dx_ref, dtype, "dx")
   check_close(dg, dg_ref, dtype, "dg")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("rev", [False, True], ids=["causal", "reverse"])
+def test_tree_walk_bits_survive_fallback(dtype, rev):
+  """The tree walk and the workspace-free walk that recomputes a call whose
+  bounded wait expired (forced with a spin limit of 0) agree with the oracle,
+  and the tree walk's bits do not depend on the launch: two calls with the
+  default spin limit are identical.  Tensors offset by one element from the
+  others (a different 16-byte phase) take the look-back walk, which must
+  agree with the oracle too."""
+  lens, C = [200000, 3, 1, 77777], 3
+  T = sum(lens)
+  g, x, dy = make(lens, C, dtype, glo=0.5, n=3)
+  gd, xd, dyd = g.to(DEV), x.to(DEV), dy.to(DEV)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  lib = _lib.load()
+
+  def run(spin=None, offset=False):
+    prev = lib.asc_set_lookback_spin_limit(spin) if spin is not None else None
+    try:
+      if offset:
+        hb = torch.empty(C * T + 1, dtype=dtype, device=DEV)
+        h = hb[1:].view(C, T)
+      else:
+        h = torch.empty_like(xd)
+      _ops.scan_fwd(gd, xd, h, cu, rev)
+      dx, dg = torch.empty_like(gd), torch.empty_like(gd)
+      _ops.scan_bwd(dyd, gd, h.contiguous(), dx, dg, cu, causal=not rev)
+      torch.cuda.synchronize()
+      return h.clone(), dx, dg
+    finally:
+      if prev is not None:
+        lib.asc_set_lookback_spin_limit(prev)
+
+  a, b = run(), run()
+  for u, w in zip(a, b):
+    assert torch.equal(u, w)
+  h_ref = oracle_fwd(g, x, lens, reverse=rev)
+  for label, res in (("tree", a), ("fallback", run(spin=0)),
+                     ("look-back", run(offset=True))):
+    h, dx, dg = res
+    check_close(h, h_ref, dtype, f"h ({label})")
+    dx_ref, dg_ref = oracle_bwd(dy, g, npf(h), lens, causal=not rev)
+    check_close(dx, dx_ref, dtype, f"dx ({label})")
+    check_close(dg, dg_ref, dtype, f"dg ({label})")
 
 
 # ---------------------------------------------------------------------------

@@ -781,24 +781,15 @@ def test_time_constant_gradient(dtype, lens, C, compiled):
     return y.detach(), gd.grad, xd.grad
 
   T = sum(lens)
-  from associative_scan_triton import _lib
-  # few items run the look-back walk for both gradients (its last bits may
-  # vary from run to run); otherwise the time-constant path must reproduce
-  # the materialised gradient bit for bit
-  lookback = _lib.load().asc_scan_workspace_bytes(
-    len(lens), C, T, _lib.dtype_code(g), 1) > 0
+  # every walk (few items: the tree walk) reads the per-row value where the
+  # dense walk reads the element, so the bits must agree
   for loss_of, dense in (
       (lambda y: y.sum().backward(), torch.ones(C, T, dtype=dtype, device=DEV)),
       (lambda y: (y.sum(-1) * w).sum().backward(),
        w[:, None].expand(C, T).contiguous())):
     y1, dg1, dx1 = grads(loss_of)
     y2, dg2, dx2 = grads(lambda y: y.backward(dense))
-    if lookback:
-      tol = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
-      torch.testing.assert_close(dx1, dx2, **tol)
-      torch.testing.assert_close(dg1, dg2, **tol)
-    else:
-      assert torch.equal(dx1, dx2) and torch.equal(dg1, dg2)
+    assert torch.equal(dx1, dx2) and torch.equal(dg1, dg2)
     dx_ref, dg_ref = oracle_bwd(dense.cpu(), g, npf(y1), lens)
     check_close(dx1, dx_ref, dtype, "dx")
     check_close(dg1, dg_ref, dtype, "dg")
@@ -823,6 +814,39 @@ def test_rowgrad_entry_point(dtype, causal):
     dx_ref, dg_ref = oracle.scan_bwd(npf(dy), npf(g), npf(h), cu_of(lens), causal)
     check_close(dx, dx_ref, dtype, "dx")
     check_close(dg, dg_ref, dtype, "dg")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "anticausal"])
+@pytest.mark.parametrize("lens,C", [([1000], 100), ([3], 120), ([5, 2], 60),
+                                    ([4099, 1], 20), ([70001], 3),
+                                    ([20000, 7, 13000], 2)],
+                         ids=["rows1000", "rows3", "rows7", "rows4100",
+                              "long", "ragged"])
+def test_tree_rowgrad_rows_in_chunk(dtype, causal, lens, C):
+  """Few items with a gradient constant along time (one value per row, rows
+  3 elements apart): the tree walk's chunks hold many short rows (rows of
+  3-7 elements share a vector) or lie in one row; the per-row read must
+  give the bits of the dense gradient and match the oracle."""
+  from associative_scan_triton import _lib, _ops
+  T = sum(lens)
+  lib = _lib.load()
+  assert lib.asc_scan_workspace_walk(len(lens), C, T, _lib.dtype_code(
+    torch.empty((), dtype=dtype)), 1) == _lib.WALK_LOOKBACK
+  g, h = make(lens, C, dtype, n=2, glo=0.5)
+  rows = torch.randn(C, 3, generator=torch.Generator().manual_seed(5)).to(dtype)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  gd, hd, rd = g.to(DEV), h.to(DEV), rows.to(DEV)
+  dx = torch.empty(C, T, dtype=dtype, device=DEV)
+  dg = torch.empty_like(dx)
+  _ops.scan_bwd_rowgrad(rd[:, 1], 3, gd, hd, dx, dg, cu, causal)
+  dy = rows[:, 1:2].expand(C, T)
+  dxd, dgd = torch.empty_like(dx), torch.empty_like(dx)
+  _ops.scan_bwd(dy.contiguous().to(DEV), gd, hd, dxd, dgd, cu, causal)
+  assert torch.equal(dx, dxd) and torch.equal(dg, dgd)
+  dx_ref, dg_ref = oracle.scan_bwd(npf(dy), npf(g), npf(h), cu_of(lens), causal)
+  check_close(dx, dx_ref, dtype, "dx")
+  check_close(dg, dg_ref, dtype, "dg")
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
