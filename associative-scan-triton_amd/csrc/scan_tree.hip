@@ -3,12 +3,13 @@
 // channels), where one wave or workgroup per item would leave most CUs idle.
 //
 // The flat array of all rows is cut into chunks of kTreeWaves (16) waves x
-// kChainU (2) sub-tiles: 8192 fp32 / 16384 fp16-bf16 elements, one
+// kTreeU (2) sub-tiles: 8192 fp32 / 16384 fp16-bf16 elements, one
 // workgroup per chunk in scan order, within 64 VGPRs so that two workgroups
 // share a CU.  A chunk that lies inside one segment takes the chained
 // walk's scan; one that holds segment or row boundaries (or a tensor end)
-// takes the per-element flags of the look-back walk (seg_common.h).  Carries between
-// chunks go through a tree of published maps in the caller's workspace:
+// takes the per-element flags of the look-back walk (seg_common.h).
+// Carries between chunks go through a tree of published maps in the
+// caller's workspace:
 //   * level 0: each chunk's map (A, X, F), F = a segment head lies inside
 //     (then the map is an inclusive value), published right after its local
 //     scan;
@@ -25,8 +26,10 @@
 //
 // Chunks are numbered by blockIdx and wait only for smaller ones.  Every
 // wait is bounded (the spin limit of asc_set_lookback_spin_limit): a wave
-// whose wait expires raises a flag in the workspace and its chunk stops,
-// as does every chunk that sees the flag, and the workspace-free walk
+// whose wait expires raises a flag in the workspace and its chunk stops
+// (all its waves together, past the barrier that hands over the carry), as
+// does every chunk that sees the flag when it polls, and the workspace-free
+// walk
 // launched behind the tree kernel, which returns at once when the flag is
 // clear, then recomputes the whole call.  Progress therefore never depends
 // on the order in which workgroups are dispatched, at no register cost in
@@ -50,8 +53,12 @@ constexpr int kTreeFan = 64;
 #define ASC_TREE_WAVES 16
 #endif
 constexpr int kTreeWaves = ASC_TREE_WAVES;
+#ifndef ASC_TREE_U
+#define ASC_TREE_U 2
+#endif
+constexpr int kTreeU = ASC_TREE_U;  // sub-tiles per wave
 constexpr int64_t kTreeChunkVec =
-    static_cast<int64_t>(kTreeWaves) * kChainU * kWave;  // vectors per chunk
+    static_cast<int64_t>(kTreeWaves) * kTreeU * kWave;  // vectors per chunk
 
 struct TreeGeo {
   LbGeo g;             // segments, tensor, phase (its tile fields unused)
@@ -80,7 +87,7 @@ template <class IO, bool REV>
 __device__ inline int64_t tree_vec(const LbGeo& g, int64_t b, int wv, int u,
                                    int lane) {
   const int64_t i = b * kTreeChunkVec +
-                    static_cast<int64_t>(wv * kChainU + u) * kWave + lane;
+                    static_cast<int64_t>(wv * kTreeU + u) * kWave + lane;
   return REV ? g.nvec - 1 - i : i;
 }
 
@@ -113,6 +120,16 @@ __device__ inline LbTile tree_classify(const LbGeo& g, int64_t b) {
   if (hd == (REV ? th - 1 : tl)) r.phead = base + hd;
   if (tl_ == (REV ? tl : th - 1)) r.ptail = base + tl_;
   return r;
+}
+
+// Whether chunk b lies inside the tensor (uniform): its vectors are then
+// loaded without per-vector bounds checks, so that every load of the chunk
+// goes out at once.
+template <class IO, bool REV>
+__device__ inline bool tree_whole(const LbGeo& g, int64_t b) {
+  const int64_t v_lo = REV ? g.nvec - (b + 1) * kTreeChunkVec : b * kTreeChunkVec;
+  return v_lo >= 0 && v_lo * IO::V - g.phase >= 0 &&
+         (v_lo + kTreeChunkVec) * IO::V - g.phase <= g.n;
 }
 
 // Loads vector vi packed; elements outside the tensor read `ident`.
@@ -234,7 +251,7 @@ __device__ inline bool tree_needs_carry(const uint32_t* valid,
                                         const uint32_t* head) {
   constexpr int V = IO::V;
 #pragma unroll
-  for (int u = 0; u < kChainU; ++u) {
+  for (int u = 0; u < kTreeU; ++u) {
     const u64 any = __builtin_amdgcn_ballot_w64(valid[u] != 0);
     if (!any) continue;
     const int l0 = __builtin_ctzll(any);
@@ -260,24 +277,32 @@ struct TreePart {
   int flags;  // bit 1: some element lies in a segment; bit 0: needs a carry
 };
 
-// What wave 0 hands the other waves after the tree step.
-struct TreeCarry {
-  float carry;
+// What wave 0 hands the other waves after the tree step: each wave's carry
+// and whether every wait succeeded.
+struct TreeMeet {
+  float carry[kTreeWaves];
   int ok;
 };
 
-template <class IO, bool REV>
-__device__ inline TreeMap tree_parts_map(const TreePart* parts, bool& need) {
-  TreeMap m{1.0f, 0.0f, 0};
-  int nc = -1;
-#pragma unroll 1
-  for (int w = 0; w < kTreeWaves; ++w) {
-    const TreePart q = parts[w];
-    lb_compose(m.a, m.x, m.f, q.a, q.x, q.f);
-    if (nc < 0 && (q.flags & 2)) nc = q.flags & 1;
-  }
-  need = nc > 0;
-  return m;
+// Wave 0's work between the chunk's two barriers: the waves' maps (one per
+// lane) are scanned across lanes, which gives the chunk's map (published by
+// the tree step, which returns the carry into the chunk) and every wave's
+// exclusive prefix, applied to that carry.  The chunk needs a carry unless
+// the first wave holding an element of some segment starts with a head.
+__device__ inline void tree_meet(const TreeGeo& tg, LbSlot* slots, int64_t b,
+                                 const TreePart* parts, int lane,
+                                 uint32_t* fail, TreeMeet* out) {
+  TreePart q{1.0f, 0.0f, 0, 0};
+  if (lane < kTreeWaves) q = parts[lane];
+  const u64 any = __builtin_amdgcn_ballot_w64((q.flags & 2) != 0);
+  const bool need =
+      any && (__builtin_amdgcn_readlane(q.flags, __builtin_ctzll(any)) & 1);
+  const SegScan s = seg_finish(q.a, q.x, q.f);
+  bool ok = true;
+  const float carry =
+      tree_step(tg, slots, b, TreeMap{s.ta, s.tx, s.tf}, need, lane, fail, ok);
+  if (lane < kTreeWaves) out->carry[lane] = seg_carry_in(s, carry);
+  if (lane == 0) out->ok = ok ? 1 : 0;
 }
 
 // The local scan of one sub-tile: the chained walk's scan when the chunk
@@ -311,20 +336,28 @@ __device__ inline SegScan tree_fwd_sub(const LbGeo& g, const LbTile& ti,
 template <class IO, bool REV>
 __device__ inline void tree_fwd_chunk(const TreeFwdParams& p, int br,
                                       int64_t b, int lane, int wv,
-                                      TreePart* parts, TreeCarry* carry_s) {
+                                      TreePart* parts, TreeMeet* meet) {
   constexpr int V = IO::V;
-  constexpr int U = kChainU;
+  constexpr int U = kTreeU;
   const LbGeo& g = p.t.g;
   const FwdPtrs& q = p.br[br];
   uint4 gq[U], xq[U];
   int64_t vi[U];
-  uint32_t inten[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    vi[u] = tree_vec<IO, REV>(g, b, wv, u, lane);
-    inten[u] = lb_inten<IO>(g, vi[u]);
-    gq[u] = tree_load<IO>(q.g, vi[u], inten[u], 1.0f);
-    xq[u] = tree_load<IO>(q.x, vi[u], inten[u], 0.0f);
+  for (int u = 0; u < U; ++u) vi[u] = tree_vec<IO, REV>(g, b, wv, u, lane);
+  if (tree_whole<IO, REV>(g, b)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      gq[u] = ld16(q.g + vi[u] * 16);
+      xq[u] = ld16(q.x + vi[u] * 16);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t inten = lb_inten<IO>(g, vi[u]);
+      gq[u] = tree_load<IO>(q.g, vi[u], inten, 1.0f);
+      xq[u] = tree_load<IO>(q.x, vi[u], inten, 0.0f);
+    }
   }
   const LbTile ti = tree_classify<IO, REV>(g, b);
   SegScan sc[U];
@@ -350,23 +383,13 @@ __device__ inline void tree_fwd_chunk(const TreeFwdParams& p, int br,
   if (lane == 0)
     parts[wv] = TreePart{wm.a, wm.x, wm.f, (any_w ? 2 : 0) | (need_w ? 1 : 0)};
   __syncthreads();
-  if (wv == 0) {
-    bool need;
-    const TreeMap m = tree_parts_map<IO, REV>(parts, need);
-    LbSlot* slots = p.slots + br * p.t.per_branch;
-    bool ok = true;
-    const float carry = tree_step(p.t, slots, b, m, need, lane, p.fail, ok);
-    if (lane == 0) *carry_s = TreeCarry{carry, ok ? 1 : 0};
-  }
+  if (wv == 0)
+    tree_meet(p.t, p.slots + br * p.t.per_branch, b, parts, lane, p.fail, meet);
   __syncthreads();
   // a failed wait: the workspace-free walk behind this launch recomputes
   // the call
-  if (!carry_s->ok) return;
-  float c = carry_s->carry;
-  for (int w = 0; w < wv; ++w) {
-    const TreePart pw = parts[w];
-    c = pw.f ? pw.x : fmaf(pw.a, c, pw.x);
-  }
+  if (!meet->ok) return;
+  float c = meet->carry[wv];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     float gf[V], xf[V], hf[V];
@@ -394,11 +417,10 @@ template <class IO, int DIRS>
 __global__ void __launch_bounds__(kTreeWaves* kWave, 8)
     k_scan_fwd_tree(TreeFwdParams p) {
   __shared__ TreePart parts[kTreeWaves];
-  __shared__ TreeCarry carry_s;
-  if (tree_failed(p.fail)) return;
+  __shared__ TreeMeet meet;
   const int lane = threadIdx.x % kWave;
   const int wv = wave_id();
-  tree_fwd_chunk<IO, DIRS == 2>(p, 0, blockIdx.x, lane, wv, parts, &carry_s);
+  tree_fwd_chunk<IO, DIRS == 2>(p, 0, blockIdx.x, lane, wv, parts, &meet);
 }
 
 // ---- backward (B order: RB = the forward was causal) ----
@@ -446,17 +468,17 @@ __device__ inline uint4 tree_dyc_vec(const char* dy, int64_t rs,
 // order, 1 outside the tensor, and the state just past its last one, 0
 // outside), the shifted gates and states cross lanes by DPP and sub-tiles
 // by readlane, and segment heads and tails reset them exactly.
-// HL: the loaded states wait for the carry in LDS (hl: kTreeWaves * kChainU
+// HL: the loaded states wait for the carry in LDS (hl: kTreeWaves * kTreeU
 // * 64 vectors), not in registers: fp16 / bf16 chunks then fit 64 VGPRs,
 // two workgroups per CU.
 // DYC: the gradient is one value per row (dy_rs), constant along time.
 template <class IO, bool RB, bool HL, bool DYC>
 __device__ inline void tree_bwd_chunk(const TreeBwdParams& p, int br,
                                       int64_t b, int lane, int wv,
-                                      TreePart* parts, TreeCarry* carry_s,
+                                      TreePart* parts, TreeMeet* meet,
                                       uint4* hl) {
   constexpr int V = IO::V;
-  constexpr int U = kChainU;
+  constexpr int U = kTreeU;
   constexpr uint32_t full = (1u << V) - 1;
   constexpr int jl = mem_idx<V, RB>(V - 1);  // last element in B order
   constexpr int jf = mem_idx<V, RB>(0);      // first element in B order
@@ -465,12 +487,22 @@ __device__ inline void tree_bwd_chunk(const TreeBwdParams& p, int br,
   uint4 yq[U], gq[U], hq[U];
   int64_t vi[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    vi[u] = tree_vec<IO, RB>(g, b, wv, u, lane);
-    const uint32_t inten = lb_inten<IO>(g, vi[u]);
-    if (!DYC) yq[u] = tree_load<IO>(q.dy, vi[u], inten, 0.0f);
-    gq[u] = tree_load<IO>(q.g, vi[u], inten, 1.0f);
-    hq[u] = tree_load<IO>(q.h, vi[u], inten, 0.0f);
+  for (int u = 0; u < U; ++u) vi[u] = tree_vec<IO, RB>(g, b, wv, u, lane);
+  if (tree_whole<IO, RB>(g, b)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!DYC) yq[u] = ld16(q.dy + vi[u] * 16);
+      gq[u] = ld16(q.g + vi[u] * 16);
+      hq[u] = ld16(q.h + vi[u] * 16);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t inten = lb_inten<IO>(g, vi[u]);
+      if (!DYC) yq[u] = tree_load<IO>(q.dy, vi[u], inten, 0.0f);
+      gq[u] = tree_load<IO>(q.g, vi[u], inten, 1.0f);
+      hq[u] = tree_load<IO>(q.h, vi[u], inten, 0.0f);
+    }
   }
   if (HL) {
 #pragma unroll
@@ -546,21 +578,11 @@ __device__ inline void tree_bwd_chunk(const TreeBwdParams& p, int br,
   if (lane == 0)
     parts[wv] = TreePart{wm.a, wm.x, wm.f, (any_w ? 2 : 0) | (need_w ? 1 : 0)};
   __syncthreads();
-  if (wv == 0) {
-    bool need;
-    const TreeMap m = tree_parts_map<IO, RB>(parts, need);
-    LbSlot* slots = p.slots + br * p.t.per_branch;
-    bool ok = true;
-    const float carry = tree_step(p.t, slots, b, m, need, lane, p.fail, ok);
-    if (lane == 0) *carry_s = TreeCarry{carry, ok ? 1 : 0};
-  }
+  if (wv == 0)
+    tree_meet(p.t, p.slots + br * p.t.per_branch, b, parts, lane, p.fail, meet);
   __syncthreads();
-  if (!carry_s->ok) return;
-  float c = carry_s->carry;
-  for (int w = 0; w < wv; ++w) {
-    const TreePart pw = parts[w];
-    c = pw.f ? pw.x : fmaf(pw.a, c, pw.x);
-  }
+  if (!meet->ok) return;
+  float c = meet->carry[wv];
   // dx first, then dg = (shifted state) * dx with the states unpacked only
   // then: g, dy and h are never unpacked at once
 #pragma unroll
@@ -628,13 +650,12 @@ template <class IO, int DIRS, bool DYC>
 __global__ void __launch_bounds__(kTreeWaves* kWave, TreeHl<IO> || IO::V == 4 ? 8 : 6)
     k_scan_bwd_tree(TreeBwdParams p) {
   __shared__ TreePart parts[kTreeWaves];
-  __shared__ TreeCarry carry_s;
-  __shared__ uint4 hl[TreeHl<IO> ? kTreeWaves * kChainU * kWave : 1];
-  if (tree_failed(p.fail)) return;
+  __shared__ TreeMeet meet;
+  __shared__ uint4 hl[TreeHl<IO> ? kTreeWaves * kTreeU * kWave : 1];
   const int lane = threadIdx.x % kWave;
   const int wv = wave_id();
   tree_bwd_chunk<IO, DIRS == 1, TreeHl<IO>, DYC>(p, 0, blockIdx.x, lane, wv,
-                                                 parts, &carry_s, hl);
+                                                 parts, &meet, hl);
 }
 
 template <class IO>
