@@ -55,6 +55,14 @@ CONFIGS = {
   "bf16": ("causal fwd+bwd, B=8 C=1536 T=65536, bf16 storage, fp32 "
            "accumulate, g~0.99+0.01U(0,1)", 8, 1536, 65536, "bfloat16", "causal",
            (0.99, 1.0)),
+  # not BASELINE configs: one long sequence in one channel (one item: the
+  # few-item tree walk), cfg5's per-tensor size / 6
+  "row": ("causal fwd+bwd, one sequence T=2^27 in one channel (few-item "
+          "walk), fp32, g~0.99+0.01U(0,1)", 1, 1, 1 << 27, "float32",
+          "causal", (0.99, 1.0)),
+  "row_bf16": ("causal fwd+bwd, one sequence T=2^27 in one channel (few-item "
+               "walk), bf16 storage, fp32 accumulate, g~0.99+0.01U(0,1)", 1, 1,
+               1 << 27, "bfloat16", "causal", (0.99, 1.0)),
   # not a BASELINE config: the segment-aware shift of _shift_pad.py at cfg5's
   # tensor size (compiled semantics, pad at segment starts)
   "shift": ("shift_pad backward=True (compiled form), B=8 C=1536 T=65536, "
