@@ -212,6 +212,25 @@ def main():
   torch.cuda.synchronize()
   fwd_ms = [e[0].elapsed_time(e[1]) for e in ev]
   bwd_ms = [e[1].elapsed_time(e[2]) for e in ev] if with_bwd else [0.0]
+
+  # ---- and once more, each step alone after a 1 GiB write that flushes
+  # the caches (four times the 256 MB MALL), as the reference's do_bench
+  # does; the median of these is reported beside the back-to-back mean ----
+  flush = torch.empty(1 << 28, dtype=torch.int32, device=dev)
+  fl = []
+  for _ in range(a.steps):
+    flush.fill_(0)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    fwd()
+    if with_bwd:
+      bwd()
+    e1.record(stream)
+    e1.synchronize()
+    fl.append(e0.elapsed_time(e1))
+  del flush
+  flushed_ms = float(np.median(fl))
   log(f"[bench] timed {a.steps} steps in {wall:.3f} s wall, "
       f"{step_ms:.4f} ms per step; per call: fwd {np.mean(fwd_ms):.4f} ms, "
       f"bwd {np.mean(bwd_ms):.4f} ms")
@@ -496,6 +515,7 @@ def main():
     "steps": a.steps,
     "warmup": a.warmup,
     "ms_per_step": round(step_ms, 4),
+    "ms_per_step_flushed_median": round(flushed_ms, 4),
     "higher_is_better": True,
     "scaling": "weak",
     "vs_baseline": None,
