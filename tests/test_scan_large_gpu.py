@@ -470,12 +470,13 @@ def test_beyond_2pow31_elements(dtype, ragged):
 
 
 def test_beyond_2pow31_elements_lookback():
-  """5 bf16 rows of 2^29 (2^31 + 2^29 elements, 15 items: the look-back
-  walk, whose in-row offsets are 32-bit).  Each row holds a long segment and
-  two short ones; the short segments of the last row lie past element 2^31
-  and are checked against the oracle; the long segments of the first and
-  last row against the workspace-free walk (one 16-wave workgroup per
-  item), forward and backward."""
+  """5 bf16 rows of 2^29 (2^31 + 2^29 elements, 15 items: the few-item
+  tree walk, 163840 chunks in three levels of slots, whose in-row offsets
+  are 32-bit).  Each row holds a long segment and two short ones; the short
+  segments of the last row lie past element 2^31 and are checked against
+  the oracle; the long segments of the first and last row against the
+  workspace-free walk (one 16-wave workgroup per item), forward and
+  backward."""
   from associative_scan_triton import _lib, _ops
   dtype = torch.bfloat16
   C, T = 5, 1 << 29
@@ -517,4 +518,77 @@ def test_beyond_2pow31_elements_lookback():
     bound = 1e-2 * (1.0 + b[:, :s0].abs())
     assert bool((err <= bound).all()), f"{name}: look-back vs workspace-free"
   del g, x, dy, out
+  torch.cuda.empty_cache()
+
+
+def _window_lens(lens, a, b):
+  """Segment lengths inside [a, b) of a row cut by `lens`, with a taken as
+  a segment start."""
+  out, t = [], 0
+  for n in lens:
+    lo, hi = max(t, a), min(t + n, b)
+    if hi > lo:
+      out.append(hi - lo)
+    t += n
+  return out
+
+
+def test_tree_walk_four_levels():
+  """3 fp32 rows of 2^30 - 8192 elements (3.2G elements, 393204 chunks of
+  8192: the tree walk with all four levels of slots; the last row lies past
+  element 2^31).  With gates in [0.5, 1) a state forgets its past within a
+  few hundred elements, so the oracle run on a window that starts 2000
+  elements early from a zero state (a segment head) gives the true states
+  inside the window far below fp32 rounding (the lost part is bounded by a
+  product of 2000 gates); the same holds for the backward with the window
+  running 2000 elements past its end.  Windows: each row's start and end,
+  the segment edges, the middle of each row (chunk, group and level-2 group
+  edges are crossed by the long segment everywhere)."""
+  from associative_scan_triton import _lib, _ops
+  C, T = 3, (1 << 30) - 8192
+  lens = [T - 5000, 4999, 1]
+  lib = _lib.load()
+  assert lib.asc_scan_workspace_walk(len(lens), C, T, 0, 1) == _lib.WALK_LOOKBACK
+  assert -(-(C * T) // 8192) > 64 ** 3  # four levels
+  W = 2000
+  gen = torch.Generator(device=DEV).manual_seed(41)
+  g = torch.rand(C, T, device=DEV, generator=gen).mul_(0.5).add_(0.5)
+  x = torch.randn(C, T, device=DEV, generator=gen)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  h = torch.empty_like(x)
+  _ops.scan_fwd(g, x, h, cu, False)
+  torch.cuda.synchronize()
+  print("[four-levels] forward done", flush=True)
+  e0 = T - 5000  # the long segment's end
+  spots = [(0, 3000), (T // 2 - 1500, T // 2 + 1500), (e0 - 3000, e0 + 10),
+           (e0 - 10, T)]
+  for row in range(C):
+    for t0, t1 in spots:
+      a = max(0, t0 - W)
+      wl = _window_lens(lens, a, t1)
+      href = oracle_fwd(g[row:row + 1, a:t1].cpu(), x[row:row + 1, a:t1].cpu(), wl)
+      check_close(h[row:row + 1, t0:t1], href[:, t0 - a:], torch.float32,
+                  f"h row {row} [{t0}, {t1})")
+  del x
+  dy = torch.randn(C, T, device=DEV, generator=gen)
+  dx, dg = torch.empty_like(h), torch.empty_like(h)
+  _ops.scan_bwd(dy, g, h, dx, dg, cu, causal=True)
+  torch.cuda.synchronize()
+  print("[four-levels] backward done", flush=True)
+  for row in range(C):
+    for t0, t1 in spots:
+      a = max(0, t0 - 1)           # h[a - 1] is the pad of the window's head
+      b = min(T, t1 + W)
+      wl = _window_lens(lens, a, b)
+      dxr, dgr = oracle.scan_bwd(npf(dy[row:row + 1, a:b]),
+                                 npf(g[row:row + 1, a:b]),
+                                 npf(h[row:row + 1, a:b]), [0] + list(
+                                   np.cumsum(wl)), True)
+      lo = t0 if t0 > 0 else 0
+      check_close(dx[row:row + 1, lo:t1], dxr[:, lo - a:t1 - a], torch.float32,
+                  f"dx row {row} [{t0}, {t1})")
+      if a < t0:  # the window's first dg uses the pad, not the true state
+        check_close(dg[row:row + 1, t0:t1], dgr[:, t0 - a:t1 - a],
+                    torch.float32, f"dg row {row} [{t0}, {t1})")
+  del g, h, dy, dx, dg
   torch.cuda.empty_cache()
