@@ -823,14 +823,27 @@ def test_rowgrad_entry_point(dtype, causal):
                                     ([20000, 7, 13000], 2)],
                          ids=["rows1000", "rows3", "rows7", "rows4100",
                               "long", "ragged"])
-def test_tree_rowgrad_rows_in_chunk(dtype, causal, lens, C):
+@pytest.mark.parametrize("spin", [None, 0], ids=["tree", "fallback"])
+def test_tree_rowgrad_rows_in_chunk(dtype, causal, lens, C, spin):
   """Few items with a gradient constant along time (one value per row, rows
   3 elements apart): the tree walk's chunks hold many short rows (rows of
   3-7 elements share a vector) or lie in one row; the per-row read must
-  give the bits of the dense gradient and match the oracle."""
+  give the bits of the dense gradient and match the oracle.  With a spin
+  limit of 0 the tree walk gives up at its first wait and the
+  workspace-free walk recomputes both calls, which must agree too."""
   from associative_scan_triton import _lib, _ops
   T = sum(lens)
   lib = _lib.load()
+  prev = lib.asc_set_lookback_spin_limit(spin) if spin is not None else None
+  try:
+    _tree_rowgrad_case(lib, dtype, causal, lens, C, T)
+  finally:
+    if prev is not None:
+      lib.asc_set_lookback_spin_limit(prev)
+
+
+def _tree_rowgrad_case(lib, dtype, causal, lens, C, T):
+  from associative_scan_triton import _lib, _ops
   assert lib.asc_scan_workspace_walk(len(lens), C, T, _lib.dtype_code(
     torch.empty((), dtype=dtype)), 1) == _lib.WALK_LOOKBACK
   g, h = make(lens, C, dtype, n=2, glo=0.5)
