@@ -29,10 +29,9 @@
 // wait is bounded (the spin limit of asc_set_lookback_spin_limit): a wave
 // whose wait expires raises a flag in the workspace and its chunk stops
 // (all its waves together, past the barrier that hands over the carry), as
-// does every chunk that sees the flag when it polls, and the workspace-free
-// walk
-// launched behind the tree kernel, which returns at once when the flag is
-// clear, then recomputes the whole call.  Progress therefore never depends
+// does every chunk that sees the flag when it polls; the workspace-free
+// walk launched behind the tree kernel, which returns at once when the
+// flag is clear, then recomputes the whole call.  Progress therefore never depends
 // on the order in which workgroups are dispatched, at no register cost in
 // the tree kernel (a fallback that recomputes a missing map inside it
 // doubled its registers); numbering chunks by a ticket taken from an atomic
@@ -49,7 +48,7 @@ namespace {
 constexpr int kTreeMaxLevels = 4;        // up to 64^4 chunks per branch
 constexpr int64_t kTreeFlagBytes = 256;  // workspace: the failure flag first
 constexpr int kTreeFan = 64;
-// Chunk shape: kTreeWaves waves x kChainU sub-tiles.
+// Chunk shape: kTreeWaves waves x kTreeU sub-tiles.
 #ifndef ASC_TREE_WAVES
 #define ASC_TREE_WAVES 16
 #endif
