@@ -580,6 +580,16 @@ struct Geometry {
   int64_t items;  // S*C items per branch
   int nbranch;
   int phase;
+  // Set when the chained walk (scan_chain.hip) runs right after this
+  // per-item walk (one wave per item) in the same call: the per-item walk
+  // clears the chained walk's slots (chain_words 64-bit words), its first
+  // wave writes *chain_flag (chain_survey), and it leaves every item
+  // whose segment has both edges on the chunk grid (chain_ch elements, a
+  // power of two) to the chained walk.  chain_ch = 0: no chained walk.
+  int64_t chain_ch;
+  unsigned long long* chain_slots;
+  int64_t chain_words;
+  uint32_t* chain_flag;
 };
 
 // Tells the compiler a value is the same in every lane (it is: all lanes
@@ -598,7 +608,76 @@ __device__ inline int64_t cu_at(const Geometry& geo, int64_t i) {
                      : static_cast<int64_t>(reinterpret_cast<const int32_t*>(geo.cu)[i]));
 }
 
-// Decodes item w; returns false for an empty segment.
+// Segments the chained walk takes when it runs after a per-item walk (see
+// Geometry::chain_ch): non-empty, inside [0, T], both edges on the chunk
+// grid of ch elements (a power of two; raw cu_seqlens values;
+// chain_common.h applies the same test).
+__device__ inline bool chain_takes(int64_t ch, int64_t T, int64_t t0,
+                                   int64_t t1) {
+  return ch > 0 && t0 >= 0 && t0 < t1 && t1 <= T && ((t0 | t1) & (ch - 1)) == 0;
+}
+
+// Survey of cu_seqlens for the chained walk: which non-empty segments
+// (after the clamping of item_range) it takes (chain_takes).  kChainAll:
+// every one (a per-item walk launched before it then has nothing to do,
+// and the chained walk may read a chunk before it looks up its segment);
+// kChainNone: none (the chained grid has nothing to do); kChainSome: some,
+// or more than smax segments (not surveyed: both walks test each item or
+// chunk on its own).  Each lane looks at 4 segments per batch of 256, its
+// loads in flight together.  Returns the same value in every lane.
+enum : uint32_t { kChainNone = 0, kChainAll = 1, kChainSome = 2 };
+constexpr int64_t kChainBatch = 4 * kWave;
+__device__ inline uint32_t chain_survey(const void* cu, int cu64, int64_t S,
+                                        int64_t T, int64_t ch, int lane,
+                                        int64_t smax) {
+  if (ch == 0 || S > smax) return kChainSome;
+  bool all = true, any = false;
+  for (int64_t base = 0; base < S; base += kChainBatch) {
+    int64_t lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int64_t s = base + k * kWave + lane;
+      lo[k] = hi[k] = 0;
+      if (s < S) {
+        lo[k] = cu64 ? reinterpret_cast<const int64_t*>(cu)[s]
+                     : reinterpret_cast<const int32_t*>(cu)[s];
+        hi[k] = cu64 ? reinterpret_cast<const int64_t*>(cu)[s + 1]
+                     : reinterpret_cast<const int32_t*>(cu)[s + 1];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int64_t t0 = lo[k] < 0 ? 0 : (lo[k] > T ? T : lo[k]);
+      const int64_t t1 = hi[k] < t0 ? t0 : (hi[k] > T ? T : hi[k]);
+      const bool taken = chain_takes(ch, T, lo[k], hi[k]);
+      if (t1 > t0 && !taken) all = false;
+      if (taken) any = true;
+    }
+  }
+  if (__builtin_amdgcn_ballot_w64(!all) == 0) return kChainAll;
+  return __builtin_amdgcn_ballot_w64(any) != 0 ? kChainSome : kChainNone;
+}
+
+// Prologue of a per-item walk launched before the chained walk (see
+// Geometry::chain_ch), for wave gw of the grid's nw: clears its share of
+// the chained walk's slots; wave 0 surveys up to kChainSurveyMax segments
+// (a loop of batches) and writes the flag the chained walk reads; returns
+// true when the walk has no item to take (one batch per wave).
+constexpr int64_t kChainSurveyMax = 16 * kChainBatch - 1;
+__device__ inline bool chain_prologue(const Geometry& geo, int64_t gw,
+                                      int64_t nw, int lane) {
+  for (int64_t i = gw * kWave + lane; i < geo.chain_words; i += nw * kWave)
+    geo.chain_slots[i] = 0ull;
+  const uint32_t sv =
+      chain_survey(geo.cu, geo.cu64, geo.S, geo.T, geo.chain_ch, lane,
+                   gw == 0 ? kChainSurveyMax : kChainBatch - 1);
+  if (gw == 0 && lane == 0) *geo.chain_flag = sv;
+  return sv == kChainAll;
+}
+
+// Decodes item w; returns false for an empty segment and, in a walk that
+// can run before the chained walk (CHAIN), for an item the chained walk
+// takes.
 // BLOCKS: channels go in blocks of kItemChanBlock; inside a block, items
 // w, w+1, ... are one segment of the block's channels, then the next
 // segment.  Waves (workgroups) that run at the same time then work on
@@ -610,6 +689,7 @@ __device__ inline int64_t cu_at(const Geometry& geo, int64_t i) {
 // the order (the BLK instantiation) from the mean segment length.
 // Otherwise: the same segment of neighbouring channels (channel-major).
 constexpr int64_t kItemChanBlock = 8;
+template <bool CHAIN = false>
 __device__ inline bool item_range(const Geometry& geo, int64_t w, int& br,
                                   int64_t& P0, int64_t& P1, int64_t& row,
                                   bool blocks) {
@@ -637,6 +717,7 @@ __device__ inline bool item_range(const Geometry& geo, int64_t w, int& br,
     c = r - s * geo.C;
   }
   int64_t t0 = cu_at(geo, s), t1 = cu_at(geo, s + 1);
+  if (CHAIN && chain_takes(geo.chain_ch, geo.T, t0, t1)) return false;
   t0 = t0 < 0 ? 0 : (t0 > geo.T ? geo.T : t0);
   t1 = t1 < t0 ? t0 : (t1 > geo.T ? geo.T : t1);
   const int64_t base = c * geo.T + geo.phase;
@@ -651,9 +732,8 @@ __device__ inline int wave_id() {
 }
 
 // skip: nullptr, or a flag in device memory that makes every workgroup
-// return at once when it is set (the chained walk ran instead; see
-// scan_chain.hip) or, with skip_if_clear, when it is clear (the tree walk
-// ran and no wait of it failed; see scan_tree.hip).
+// return at once when it is set or, with skip_if_clear, when it is clear
+// (the tree walk ran and no wait of it failed; see scan_tree.hip).
 struct FwdParams {
   Geometry geo;
   FwdPtrs br[2];
@@ -674,10 +754,10 @@ __device__ inline bool skipped(const Params& p) {
   return p.skip != nullptr && ((*p.skip != 0u) != (p.skip_if_clear != 0));
 }
 
-// Grid of a per-item walk launched behind the chained walk (usually
-// skipped): at most 131072 waves (512 per CU), the grid-stride loops take
-// the rest, so that the skip costs a bounded number of workgroups, not one
-// per item.  A tighter cap hands each workgroup several ragged items when
+// Grid of a per-item walk that is usually skipped (behind the tree walk)
+// or left to the chained walk launched after it: at most 131072 waves (512
+// per CU), the grid-stride loops take the rest, so that the skip costs a
+// bounded number of workgroups, not one per item.  A tighter cap hands each workgroup several ragged items when
 // the walk does run (varlen, 32 segments of 1000-15000 fp32 elements x 1024
 // rows, 8-wave walk: 32768 waves 807 / 1201 us fwd / bwd, 131072 waves
 // 726 / 1048, uncapped 721 / 1011); a looser one costs more when skipped
@@ -686,7 +766,8 @@ constexpr int64_t kSkippableWaves = 131072;
 template <class Params>
 inline int64_t walk_grid(const Params& p, int64_t blocks, int waves_per_block) {
   const int64_t cap = kSkippableWaves / waves_per_block;
-  return p.skip != nullptr && blocks > cap ? cap : blocks;
+  return (p.skip != nullptr || p.geo.chain_ch > 0) && blocks > cap ? cap
+                                                                   : blocks;
 }
 
 // DYC: the gradient of row c of branch br is the one value
@@ -856,18 +937,17 @@ bool tree_bwd(const BwdParams& p, int dtype, int dirs, bool aln, bool dyc,
 
 // scan_chain.hip: chained chunks for segments aligned to the chunk size.
 // chain_bytes: its workspace (0 when the geometry cannot use it).
-// chain_fwd / chain_bwd return false (nothing launched) when the workspace is
-// missing or too small; otherwise they launch the chained walk, which checks
-// cu_seqlens on the device and runs only when every segment edge is
-// chunk-aligned, and set *skip to a device flag that is nonzero exactly
-// when it ran: the caller then launches its usual walk with that flag.
+// chain_plan returns false when the geometry or the workspace rules the
+// walk out; otherwise it sets g.chain_* (see Geometry), and the caller
+// launches its per-item walk with that geometry (it clears the slots and
+// walks the unaligned segments), then chain_fwd / chain_bwd (the chunks of
+// the aligned ones).
 int64_t chain_bytes(int64_t S, int64_t C, int64_t T, int v, int nbranch);
-bool chain_fwd(const FwdParams& p, int dtype, bool aln, int dirs, void* ws,
-               int64_t ws_bytes, void* stream, int& status,
-               const uint32_t** skip);
-bool chain_bwd(const BwdParams& p, int dtype, bool aln, bool dyc, int dirs,
-               void* ws, int64_t ws_bytes, void* stream, int& status,
-               const uint32_t** skip);
+bool chain_plan(Geometry& g, bool aln, int dtype, void* ws, int64_t ws_bytes,
+                bool bwd);
+int chain_fwd(const FwdParams& p, int dtype, int dirs, void* stream);
+int chain_bwd(const BwdParams& p, int dtype, bool dyc, int dirs,
+              void* stream);
 
 // scan_recompute.hip: the backward that recomputes the forward states from
 // its inputs and per-chunk checkpoints (asc_scan_bwd_recompute).

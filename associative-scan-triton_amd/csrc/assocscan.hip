@@ -119,6 +119,7 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
   // the look-back walks do not write the gate product and are not used in
   // place; they need the caller's workspace (else the per-item walks run)
   const bool walks_ok = !wa && !inplace;
+  bool chained = false;
   if (walks_ok && lb_use(S, C, T, nbranch, v)) {
     // few items: the tree walk (deterministic), or the look-back walk for
     // tensors of different phases
@@ -130,14 +131,18 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
     } else if (lb_fwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st)) {
       return st;
     }
-  } else if (walks_ok && chain_fwd(p, dtype, aln, dirs, ws, ws_bytes, stream,
-                                   st, &p.skip)) {
-    // the per-item walk below runs only if cu_seqlens turns out unaligned
-    if (st) return st;
+  } else if (walks_ok) {
+    // long segments: the per-item walk below takes the unaligned ones, the
+    // chained walk after it the chunk-aligned ones
+    chained = chain_plan(p.geo, aln, dtype, ws, ws_bytes, false);
   }
-  const int nw = wa ? 0 : pick_walk(S, C, T, nbranch, v, false);
-  if (nw) return wg_fwd(p, nw, dtype, dirs, aln, stream);
-  return item_fwd(p, dtype, dirs, aln, wa, stream);
+  // (the chained walk's partner is the one-wave walk: its launch costs a
+  // few microseconds when it has nothing to do, the workgroup walks' 20-30)
+  const int nw = wa || chained ? 0 : pick_walk(S, C, T, nbranch, v, false);
+  st = nw ? wg_fwd(p, nw, dtype, dirs, aln, stream)
+          : item_fwd(p, dtype, dirs, aln, wa, stream);
+  if (st || !chained) return st;
+  return chain_fwd(p, dtype, dirs, stream);
 }
 
 // dyc: dy[b] holds one gradient value per row (element stride dy_rs[b]
@@ -208,6 +213,7 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
   // few items: the tree walk, else (tensors of different phases) the
   // look-back walk, which takes dense gradients only
   const bool few = !inplace && lb_use(S, C, T, nbranch, v);
+  bool chained = false;
   if (few && ASC_USE_TREE &&
       tree_bwd(p, dtype, dirs, aln, dyc, ws, ws_bytes, stream, st, &p.skip)) {
     // the workspace-free walk below runs only if a tree wait failed
@@ -215,14 +221,15 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
     p.skip_if_clear = 1;
   } else if (few && !dyc) {
     if (lb_bwd(p, dtype, dirs, aln, ws, ws_bytes, stream, st)) return st;
-  } else if (!inplace && chain_bwd(p, dtype, aln, dyc, dirs, ws, ws_bytes,
-                                   stream, st, &p.skip)) {
-    // the per-item walk below runs only if cu_seqlens turns out unaligned
-    if (st) return st;
+  } else if (!inplace) {
+    // as in run_fwd: the per-item walk, then the chained walk
+    chained = chain_plan(p.geo, aln, dtype, ws, ws_bytes, true);
   }
-  const int nw = pick_walk(S, C, T, nbranch, v, true);
-  if (nw) return wg_bwd(p, nw, dtype, dirs, aln, dyc, stream);
-  return item_bwd(p, dtype, dirs, aln, dyc, stream);
+  const int nw = chained ? 0 : pick_walk(S, C, T, nbranch, v, true);
+  st = nw ? wg_bwd(p, nw, dtype, dirs, aln, dyc, stream)
+          : item_bwd(p, dtype, dirs, aln, dyc, stream);
+  if (st || !chained) return st;
+  return chain_bwd(p, dtype, dyc, dirs, stream);
 }
 
 // ---------------------------------------------------------------------------

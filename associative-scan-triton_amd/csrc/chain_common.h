@@ -1,7 +1,7 @@
 // Shared pieces of the chained-chunk walks (scan_chain.hip: the plain
 // forward and backward; scan_recompute.hip: the backward that recomputes the
 // forward states): the chunk shape, the tagged carry slots and their fixed
-// composition order, the device-side alignment check, and the host-side
+// composition order, which segments the walk takes, and the host-side
 // geometry conditions.  See scan_chain.hip for the walk itself.
 #ifndef ASC_CHAIN_COMMON_H
 #define ASC_CHAIN_COMMON_H
@@ -19,8 +19,8 @@ namespace {
 // wave (8 or 16 waves) 4.2-5.2 forward.
 constexpr int kChainWaves = 8;  // waves per workgroup (one chunk)
 constexpr int kChainU = 2;      // sub-tiles per wave
-constexpr int64_t kChainFlagBytes = 256;  // workspace: flag word, then slots
 constexpr int kChainBlock = 64;           // chunks per checkpoint
+constexpr int64_t kChainFlagBytes = 256;  // workspace: flag word, then slots
 
 // fp16/bf16 chunks keep their loaded vectors packed while the chunk waits
 // for its carry and unpack them again to apply it (fp32 unpacking is a
@@ -45,7 +45,8 @@ struct ChainGeo {
   int64_t nchunks;  // chunks per branch (C * kr)
   int nbranch;
   uint32_t spin;
-  const uint32_t* ok;  // set by the setup kernel: every edge chunk-aligned
+  // written by the per-item walk launched before (chain_survey)
+  const uint32_t* survey;
 };
 
 __device__ inline int64_t chain_cu(const ChainGeo& g, int64_t i) {
@@ -70,6 +71,10 @@ __device__ inline int64_t chain_seg(const ChainGeo& g, int64_t t) {
 
 // Where chunk b (scan order within its branch) lies.  rev: the scan runs
 // from high to low addresses, so the row's chunks are numbered from its end.
+// Returns false unless the segment holding the chunk's first element lies
+// inside [0, T] with both edges on the chunk grid (then it holds the whole
+// chunk); the per-item walk launched before the chained walk takes every
+// other segment (chain_takes applies the same test).
 struct ChainChunk {
   int64_t row, t0;  // row and row offset of the chunk's first element
   int64_t e0;       // element index (phase 0) of that element
@@ -89,12 +94,23 @@ __device__ inline bool chain_chunk(const ChainGeo& g, int64_t b, bool rev,
   const int64_t s = chain_seg(g, k.t0);
   if (s < 0 || s >= g.S) return false;
   const int64_t s0 = chain_cu(g, s), s1 = chain_cu(g, s + 1);
+  if (!chain_takes(CH, g.T, s0, s1)) return false;
   k.P0 = k.row * g.T + s0;
   k.P1 = k.row * g.T + s1;
   k.j = rev ? (s1 - k.t0 - CH) / CH : (k.t0 - s0) / CH;
   k.first_mem = k.t0 == s0;
   k.last_mem = k.t0 + CH == s1;
   return true;
+}
+
+// What the per-item walk launched before found (chain_survey; one scalar
+// load).  kChainAll: a chunk lies inside one segment or outside all, so its
+// vectors are read whole before the segment is looked up.  kChainSome: the
+// chunk looks up its segment first and reads its vectors only if the
+// chained walk takes it (the per-item walk took the others).  kChainNone:
+// nothing to do.
+__device__ inline uint32_t chain_survey_of(const ChainGeo& g) {
+  return __builtin_amdgcn_readfirstlane(*g.survey);
 }
 
 // Publishes a chunk's map right after its local scan: chunk 0 holds the
@@ -170,31 +186,6 @@ __device__ float chain_prefix_bwd(const BwdPtrs& t, const ChainChunk& k,
   return carry;
 }
 
-// Zeroes the slots; block 0 also sets *ok to 1 exactly when cu_seqlens is
-// non-decreasing, inside [0, T] and a multiple of the chunk size throughout.
-__global__ void __launch_bounds__(256)
-    k_chain_setup(u64* slots, int64_t nwords, const void* cu, int cu64,
-                  int64_t S, int64_t T, int64_t CH, uint32_t* ok) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-       i < nwords; i += stride)
-    slots[i] = 0;
-  if (blockIdx.x != 0) return;
-  int good = 1;
-  for (int64_t s = threadIdx.x; s <= S; s += 256) {
-    const int64_t v = cu64 ? reinterpret_cast<const int64_t*>(cu)[s]
-                           : reinterpret_cast<const int32_t*>(cu)[s];
-    if (v < 0 || v > T || v % CH != 0) good = 0;
-    if (s > 0) {
-      const int64_t pv = cu64 ? reinterpret_cast<const int64_t*>(cu)[s - 1]
-                              : reinterpret_cast<const int32_t*>(cu)[s - 1];
-      if (pv > v) good = 0;
-    }
-  }
-  good = __syncthreads_and(good);
-  if (threadIdx.x == 0) *ok = good ? 1u : 0u;
-}
-
 // Chunks per row when the geometry can take the chained walk: rows a
 // multiple of the chunk size, a mean segment of 1 to kChainMaxMean chunks
 // (32 for the backward), one workgroup per chunk within the grid limit; 0
@@ -222,7 +213,7 @@ int64_t chain_rows(int64_t S, int64_t C, int64_t T, int v, int nbranch,
   return kr;
 }
 
-ChainGeo chain_geo(const Geometry& g, int v, void* ws) {
+ChainGeo chain_geo(const Geometry& g, int v) {
   ChainGeo q{};
   q.cu = g.cu;
   q.cu64 = g.cu64;
@@ -233,25 +224,8 @@ ChainGeo chain_geo(const Geometry& g, int v, void* ws) {
   q.nchunks = g.C * q.kr;
   q.nbranch = g.nbranch;
   q.spin = lb_spin_limit();
-  q.ok = static_cast<const uint32_t*>(ws);
+  q.survey = g.chain_flag;
   return q;
-}
-
-int chain_setup(const ChainGeo& q, int v, void* ws, void* stream) {
-  u64* slots = reinterpret_cast<u64*>(static_cast<char*>(ws) + kChainFlagBytes);
-  int64_t nwords = q.nchunks * q.nbranch * static_cast<int64_t>(sizeof(LbSlot) / 8);
-  int64_t blocks = (nwords + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  if (blocks < 1) blocks = 1;
-  const void* cu = q.cu;
-  int cu64 = q.cu64;
-  int64_t S = q.S, T = q.T, CH = chain_elems(v);
-  uint32_t* ok = static_cast<uint32_t*>(ws);
-  void* args[] = {&slots, &nwords, &cu, &cu64, &S, &T, &CH, &ok};
-  const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&k_chain_setup),
-                                       dim3(static_cast<unsigned>(blocks)), dim3(256),
-                                       args, 0, static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? ASC_OK : static_cast<int>(e);
 }
 
 int64_t chain_need(int64_t C, int64_t kr, int nbranch) {
@@ -266,6 +240,21 @@ bool chain_ready(const Geometry& g, bool aln, int v, void* ws,
   if (!aln || g.phase != 0) return false;
   const int64_t kr = chain_rows(g.S, g.C, g.T, v, g.nbranch, bwd);
   return kr > 0 && ws_bytes >= chain_need(g.C, kr, g.nbranch);
+}
+
+// When the chained walk takes the call: sets g.chain_* so that the
+// per-item walk launched first writes the flag word at the start of ws,
+// clears the slots after it and leaves the chunk-aligned segments to it.
+bool chain_share(Geometry& g, bool aln, int v, void* ws, int64_t ws_bytes,
+                 bool bwd) {
+  if (!chain_ready(g, aln, v, ws, ws_bytes, bwd)) return false;
+  const int64_t kr = g.T / chain_elems(v);
+  g.chain_ch = chain_elems(v);
+  g.chain_flag = static_cast<uint32_t*>(ws);
+  g.chain_slots = reinterpret_cast<u64*>(static_cast<char*>(ws) + kChainFlagBytes);
+  g.chain_words = (chain_need(g.C, kr, g.nbranch) - kChainFlagBytes) /
+                  static_cast<int64_t>(sizeof(u64));
+  return true;
 }
 
 }  // namespace

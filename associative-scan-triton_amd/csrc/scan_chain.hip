@@ -24,10 +24,12 @@
 // progress never depends on workgroup scheduling (that carry is composed in
 // another order, so only such a pathological wait changes the last bits).
 //
-// The host cannot see cu_seqlens, so a setup kernel checks on the device
-// that every edge is chunk-aligned (and zeroes the slots); the chained walk
-// runs only then, and the workgroup / one-wave walk launched after it with
-// the same flag runs only otherwise.
+// The host cannot see cu_seqlens, so the call first launches the
+// workgroup / one-wave walk, which clears the slots and walks the items of
+// every segment whose edges are not both on the chunk grid; the chained
+// walk then takes the chunks of the other segments (both kernels apply the
+// same test to the same cu_seqlens values).  Where every edge is aligned
+// the first launch only clears the slots.
 
 #include "chain_common.h"
 
@@ -80,8 +82,12 @@ __device__ inline void chain_fwd_chunk(const ChainFwdParams& p, int br,
   constexpr int64_t CH = chain_elems(V);
   ChainChunk k;
   const FwdPtrs& t = p.br[br];
-  // the chunk lies inside one segment or outside all (aligned edges), so
-  // its vectors are read whole before the segment is looked up
+  // read the chunk before its segment is looked up when every segment is
+  // chunk-aligned (chain_survey_of)
+  const uint32_t sv = chain_survey_of(p.geo);
+  if (sv == kChainNone) return;
+  const bool all = sv == kChainAll;
+  if (!all && !chain_chunk<CH>(p.geo, b, REV, k)) return;
   k.row = b / p.geo.kr;
   {
     const int64_t rr = b - k.row * p.geo.kr;
@@ -96,7 +102,7 @@ __device__ inline void chain_fwd_chunk(const ChainFwdParams& p, int br,
     gq[u] = ld16(t.g + vi[u] * 16);
     xq[u] = ld16(t.x + vi[u] * 16);
   }
-  if (!chain_chunk<CH>(p.geo, b, REV, k)) return;  // outside every segment
+  if (all && !chain_chunk<CH>(p.geo, b, REV, k)) return;  // outside all
   const int64_t head = REV ? k.P1 - 1 : k.P0;
   const bool hsub = k.j == 0 && wv == 0;  // sub-tile 0 of wave 0 holds the head
   SubScan sc[U];
@@ -163,7 +169,6 @@ __global__ void __launch_bounds__(kChainWaves* kWave, IO::V == 4 ? 1 : 8)
     k_scan_fwd_chain(ChainFwdParams p) {
   __shared__ float2 agg[kChainWaves];
   __shared__ float carry_s;
-  if (*p.geo.ok == 0u) return;
   const int lane = threadIdx.x % kWave;
   const int wv = wave_id();
   const int64_t gb = blockIdx.x;
@@ -187,6 +192,11 @@ __device__ inline void chain_bwd_chunk(const ChainBwdParams& p, int br,
   constexpr int jf = mem_idx<V, RB>(0);      // first element in B order
   ChainChunk k;
   const BwdPtrs& t = p.br[br];
+  // as in chain_fwd_chunk
+  const uint32_t sv = chain_survey_of(p.geo);
+  if (sv == kChainNone) return;
+  const bool all = sv == kChainAll;
+  if (!all && !chain_chunk<CH>(p.geo, b, RB, k)) return;
   k.row = b / p.geo.kr;
   {
     const int64_t rr = b - k.row * p.geo.kr;
@@ -214,7 +224,7 @@ __device__ inline void chain_bwd_chunk(const ChainBwdParams& p, int br,
       IO::unpack(yq[u], y);
     }
   };
-  if (!chain_chunk<CH>(p.geo, b, RB, k)) return;
+  if (all && !chain_chunk<CH>(p.geo, b, RB, k)) return;
   const int64_t head = RB ? k.P1 - 1 : k.P0;  // B-order head and tail
   const int64_t tail = RB ? k.P0 : k.P1 - 1;
   const bool tail_chunk = RB ? k.first_mem : k.last_mem;
@@ -306,7 +316,6 @@ __global__ void __launch_bounds__(kChainWaves* kWave)
     k_scan_bwd_chain(ChainBwdParams p) {
   __shared__ float2 agg[kChainWaves];
   __shared__ float carry_s;
-  if (*p.geo.ok == 0u) return;
   const int lane = threadIdx.x % kWave;
   const int wv = wave_id();
   const int64_t gb = blockIdx.x;
@@ -346,16 +355,16 @@ int64_t chain_bytes(int64_t S, int64_t C, int64_t T, int v, int nbranch) {
   return kr == 0 ? 0 : chain_need(C, kr, nbranch);
 }
 
-bool chain_fwd(const FwdParams& p, int dtype, bool aln, int dirs, void* ws,
-               int64_t ws_bytes, void* stream, int& status,
-               const uint32_t** skip) {
+bool chain_plan(Geometry& g, bool aln, int dtype, void* ws, int64_t ws_bytes,
+                bool bwd) {
+  return chain_share(g, aln, 16 / elem_size(dtype), ws, ws_bytes, bwd);
+}
+
+int chain_fwd(const FwdParams& p, int dtype, int dirs, void* stream) {
   const int v = 16 / elem_size(dtype);
-  if (!chain_ready(p.geo, aln, v, ws, ws_bytes, false)) return false;
   ChainFwdParams q{};
-  q.geo = chain_geo(p.geo, v, ws);
-  for (int b = 0; b < p.geo.nbranch; ++b) q.br[b] = p.br[b];
-  q.slots = reinterpret_cast<LbSlot*>(static_cast<char*>(ws) + kChainFlagBytes);
-  if ((status = chain_setup(q.geo, v, ws, stream))) return true;
+  q.geo = chain_geo(p.geo, v);
+  q.slots = reinterpret_cast<LbSlot*>(p.geo.chain_slots);
   // one launch per branch (both branches in one grid measured slower)
   auto one = [&](int b, int d) {
     ChainFwdParams r = q;
@@ -370,25 +379,17 @@ bool chain_fwd(const FwdParams& p, int dtype, bool aln, int dirs, void* ws,
     }
     return launch(fn, r.geo.nchunks, kChainWaves, r, stream);
   };
-  status = dirs == 3 ? one(0, 1) : one(0, dirs);
+  int status = dirs == 3 ? one(0, 1) : one(0, dirs);
   if (status == ASC_OK && dirs == 3) status = one(1, 2);
-  *skip = static_cast<const uint32_t*>(ws);
-  return true;
+  return status;
 }
 
-bool chain_bwd(const BwdParams& p, int dtype, bool aln, bool dyc, int dirs,
-               void* ws, int64_t ws_bytes, void* stream, int& status,
-               const uint32_t** skip) {
+int chain_bwd(const BwdParams& p, int dtype, bool dyc, int dirs,
+              void* stream) {
   const int v = 16 / elem_size(dtype);
-  if (!chain_ready(p.geo, aln, v, ws, ws_bytes, true)) return false;
   ChainBwdParams q{};
-  q.geo = chain_geo(p.geo, v, ws);
-  for (int b = 0; b < p.geo.nbranch; ++b) {
-    q.br[b] = p.br[b];
-    q.dy_rs[b] = p.dy_rs[b];
-  }
-  q.slots = reinterpret_cast<LbSlot*>(static_cast<char*>(ws) + kChainFlagBytes);
-  if ((status = chain_setup(q.geo, v, ws, stream))) return true;
+  q.geo = chain_geo(p.geo, v);
+  q.slots = reinterpret_cast<LbSlot*>(p.geo.chain_slots);
   auto one = [&](int b, int d) {
     ChainBwdParams r = q;
     r.geo.nbranch = 1;
@@ -403,10 +404,9 @@ bool chain_bwd(const BwdParams& p, int dtype, bool aln, bool dyc, int dirs,
     }
     return launch(fn, r.geo.nchunks, kChainWaves, r, stream);
   };
-  status = dirs == 3 ? one(0, 1) : one(0, dirs);
+  int status = dirs == 3 ? one(0, 1) : one(0, dirs);
   if (status == ASC_OK && dirs == 3) status = one(1, 2);
-  *skip = static_cast<const uint32_t*>(ws);
-  return true;
+  return status;
 }
 
 }  // namespace asc

@@ -15,6 +15,11 @@
 namespace asc {
 namespace {
 
+// Pipeline depths (sub-tiles per block): deep for long items
+// (scan_item.hip), shallow for short ones (scan_item_short.hip).  Only the
+// deep kernels (16-byte aligned tensors, no gate product) can run before
+// the chained walk, which takes segments of a chunk or more.
+constexpr int kFwdDeep = 4, kBwdDeep = 2, kFwdShallow = 2, kBwdShallow = 1;
 
 template <class IO, bool REV, bool ALN, bool WA, bool MASKED, int NS>
 __device__ inline void fwd_block(const FwdPtrs& t, const Walk<IO, REV>& w,
@@ -247,15 +252,20 @@ __device__ void bwd_item(const BwdPtrs& t, int64_t P0, int64_t P1, int lane,
 // occupancy).
 template <class IO, int DIRS, bool ALN, bool WA, int U>
 __global__ void __launch_bounds__(kWPB* kWave) k_scan_fwd(FwdParams p) {
+  constexpr bool CHAIN = ALN && !WA && U == kFwdDeep;
   if (skipped(p)) return;
   const int lane = threadIdx.x % kWave;
   const int64_t W = p.geo.items * p.geo.nbranch;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kWPB;
+  if (CHAIN && p.geo.chain_ch > 0 &&
+      chain_prologue(p.geo, static_cast<int64_t>(blockIdx.x) * kWPB + wave_id(),
+                     stride, lane))
+    return;
   for (int64_t w = static_cast<int64_t>(blockIdx.x) * kWPB + wave_id(); w < W;
        w += stride) {
     int br;
     int64_t P0, P1, row;
-    if (!item_range(p.geo, w, br, P0, P1, row, true)) continue;
+    if (!item_range<CHAIN>(p.geo, w, br, P0, P1, row, true)) continue;
     const FwdPtrs& t = p.br[br];
     if (DIRS == 1 || (DIRS == 3 && br == 0))
       fwd_item<IO, false, ALN, WA, U>(t, P0, P1, lane);
@@ -269,15 +279,20 @@ __global__ void __launch_bounds__(kWPB* kWave) k_scan_fwd(FwdParams p) {
 // 3 = branch 0 causal / branch 1 reverse.
 template <class IO, int DIRS, bool ALN, bool DYC, int U>
 __global__ void __launch_bounds__(kWPB* kWave) k_scan_bwd(BwdParams p) {
+  constexpr bool CHAIN = ALN && U == kBwdDeep;
   if (skipped(p)) return;
   const int lane = threadIdx.x % kWave;
   const int64_t W = p.geo.items * p.geo.nbranch;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kWPB;
+  if (CHAIN && p.geo.chain_ch > 0 &&
+      chain_prologue(p.geo, static_cast<int64_t>(blockIdx.x) * kWPB + wave_id(),
+                     stride, lane))
+    return;
   for (int64_t w = static_cast<int64_t>(blockIdx.x) * kWPB + wave_id(); w < W;
        w += stride) {
     int br;
     int64_t P0, P1, row;
-    if (!item_range(p.geo, w, br, P0, P1, row, true)) continue;
+    if (!item_range<CHAIN>(p.geo, w, br, P0, P1, row, true)) continue;
     const BwdPtrs& t = p.br[br];
     const float dyv = dyc_value<IO, DYC>(p, br, row);
     if (DIRS == 1 || (DIRS == 3 && br == 0))

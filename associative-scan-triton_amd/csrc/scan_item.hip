@@ -7,9 +7,6 @@
 namespace asc {
 namespace {
 
-// Pipeline depth (sub-tiles per block) of the long-item kernels.
-constexpr int kFwdUnroll = 4, kBwdUnroll = 2;
-
 // Short items: a mean segment of at most 4 sub-tiles (fp32 backward: 3).  Their waves run the shallow-pipeline kernels, whose lower
 // register count admits more waves per SIMD (fp32 forward 93 -> 57 VGPRs,
 // bf16 backward 125 -> 96).  Measured on MI355X, uniform segments of
@@ -37,9 +34,9 @@ int item_fwd(FwdParams p, int dtype, int dirs, bool aln, bool wa,
     fn = item_fwd_short_kernel(dtype, dirs, aln, wa);
   } else {
     switch (dtype) {
-      case ASC_F32: fn = pick_fwd<IoF32, kFwdUnroll>(dirs, aln, wa); break;
-      case ASC_F16: fn = pick_fwd<IoF16, kFwdUnroll>(dirs, aln, wa); break;
-      default: fn = pick_fwd<IoBF16, kFwdUnroll>(dirs, aln, wa); break;
+      case ASC_F32: fn = pick_fwd<IoF32, kFwdDeep>(dirs, aln, wa); break;
+      case ASC_F16: fn = pick_fwd<IoF16, kFwdDeep>(dirs, aln, wa); break;
+      default: fn = pick_fwd<IoBF16, kFwdDeep>(dirs, aln, wa); break;
     }
   }
   const int64_t items = p.geo.items * p.geo.nbranch;
@@ -53,9 +50,9 @@ int item_bwd(BwdParams p, int dtype, int dirs, bool aln, bool dyc,
     fn = item_bwd_short_kernel(dtype, dirs, aln, dyc);
   } else {
     switch (dtype) {
-      case ASC_F32: fn = pick_bwd<IoF32, kBwdUnroll>(dirs, aln, dyc); break;
-      case ASC_F16: fn = pick_bwd<IoF16, kBwdUnroll>(dirs, aln, dyc); break;
-      default: fn = pick_bwd<IoBF16, kBwdUnroll>(dirs, aln, dyc); break;
+      case ASC_F32: fn = pick_bwd<IoF32, kBwdDeep>(dirs, aln, dyc); break;
+      case ASC_F16: fn = pick_bwd<IoF16, kBwdDeep>(dirs, aln, dyc); break;
+      default: fn = pick_bwd<IoBF16, kBwdDeep>(dirs, aln, dyc); break;
     }
   }
   const int64_t items = p.geo.items * p.geo.nbranch;

@@ -25,12 +25,13 @@
 //   3. each wave composes its backward carry and writes dx, dg.
 // Two walks use it:
 //   * chained (k_scan_bwd_rc_chain): one workgroup per chunk with the
-//     chained walk's slots, for segments aligned to the chunk grid (checked
+//     chained walk's slots, for segments aligned to the chunk grid (tested
 //     on the device, as in scan_chain.hip);
 //   * per item (k_scan_bwd_rc_item): one workgroup per (segment, channel)
 //     item looping over the chunks the segment touches in B order (edges
 //     masked per element), the carry in registers; it runs for every other
-//     geometry and when the alignment check fails.
+//     geometry, and before the chained walk for the unaligned segments
+//     (clearing the chained walk's slots first).
 //
 // Reference semantics: the same fused backward as _kernels.py:171-287 (the
 // states the reference saves in scan_eager.py:42-47 are recomputed instead
@@ -55,7 +56,11 @@ struct RcParams {
   RcPtrs t;
   int64_t dy_rs;         // DYC: element stride between rows of dy
   LbSlot* slots;         // chained walk
-  const uint32_t* skip;  // per-item walk: skip when set (the chained walk ran)
+  // per-item walk before the chained walk: Geometry::chain_*
+  int64_t chain_ch;
+  unsigned long long* chain_slots;
+  int64_t chain_words;
+  uint32_t* chain_flag;
 };
 
 __device__ inline float lane_mirror(float v, int lane) {
@@ -291,6 +296,12 @@ __device__ inline void rc_chain_chunk(const RcParams& p, int64_t b, int lane,
   constexpr int V = IO::V;
   constexpr int64_t CH = chain_elems(V);
   ChainChunk k;
+  // read the chunk before its segment is looked up when every segment is
+  // chunk-aligned (chain_survey_of)
+  const uint32_t sv = chain_survey_of(p.geo);
+  if (sv == kChainNone) return;
+  const bool all = sv == kChainAll;
+  if (!all && !chain_chunk<CH>(p.geo, b, RB, k)) return;
   k.row = b / p.geo.kr;
   {
     const int64_t rr = b - k.row * p.geo.kr;
@@ -298,10 +309,9 @@ __device__ inline void rc_chain_chunk(const RcParams& p, int64_t b, int lane,
   }
   const float dyv =
       DYC ? IO::load1(p.t.dy + k.row * p.dy_rs * IO::ES) : 0.0f;
-  // the chunk lies inside one segment or outside all (aligned edges)
   RcWave<IO> s;
   rc_load_chunk<IO, RB, DYC, false>(p.t, k.e0, 0, 0, wv, lane, s);
-  if (!chain_chunk<CH>(p.geo, b, RB, k)) return;  // outside every segment
+  if (all && !chain_chunk<CH>(p.geo, b, RB, k)) return;  // outside all
   const int64_t bhead = RB ? k.P1 - 1 : k.P0;
   const int64_t btail = RB ? k.P0 : k.P1 - 1;
   const bool tail_chunk = RB ? k.first_mem : k.last_mem;
@@ -361,7 +371,6 @@ template <class IO, int DIRS, bool DYC>
 __global__ void __launch_bounds__(kChainWaves* kWave)
     k_scan_bwd_rc_chain(RcParams p) {
   __shared__ RcLds L;
-  if (*p.geo.ok == 0u) return;
   const int lane = threadIdx.x % kWave;
   const int wv = wave_id();
   rc_chain_chunk<IO, DIRS == 1, DYC>(p, blockIdx.x, lane, wv, L);
@@ -429,15 +438,20 @@ template <class IO, int DIRS, bool DYC>
 __global__ void __launch_bounds__(kChainWaves* kWave)
     k_scan_bwd_rc_item(RcParams p) {
   __shared__ RcLds L;
-  if (p.skip != nullptr && *p.skip != 0u) return;
   const int lane = threadIdx.x % kWave;
   const int wv = wave_id();
-  Geometry geo{p.geo.cu, p.geo.cu64, p.geo.S, p.geo.C, p.geo.T,
-               p.geo.S * p.geo.C, 1, 0};
+  Geometry geo{p.geo.cu,    p.geo.cu64,    p.geo.S,       p.geo.C,
+               p.geo.T,     p.geo.S * p.geo.C, 1,         0,
+               p.chain_ch,  p.chain_slots, p.chain_words, p.chain_flag};
+  // the same value in every wave of the workgroup: all return together
+  if (geo.chain_ch > 0 &&
+      chain_prologue(geo, static_cast<int64_t>(blockIdx.x) * kChainWaves + wv,
+                     static_cast<int64_t>(gridDim.x) * kChainWaves, lane))
+    return;
   for (int64_t w = blockIdx.x; w < geo.items; w += gridDim.x) {
     int br;
     int64_t P0, P1, row;
-    if (!item_range(geo, w, br, P0, P1, row, true)) continue;
+    if (!item_range<true>(geo, w, br, P0, P1, row, true)) continue;
     rc_item<IO, DIRS == 1, DYC>(p, P0, P1, row, lane, wv, L);
   }
 }
@@ -546,28 +560,30 @@ int rc_bwd(const RcArgs& a, void* stream) {
                static_cast<char*>(a.dg), a.ckpt};
   p.dy_rs = a.dy_rs;
   const bool dyc = a.dy_rs >= 0;
-  int st = ASC_OK;
-  // the chained walk for chunk-aligned long segments (checked on the
-  // device); the per-item walk behind it runs only when the check fails
-  if (!a.inplace && chain_ready(g, true, v, a.ws, a.ws_bytes, true)) {
-    p.geo = chain_geo(g, v, a.ws);
-    p.slots = reinterpret_cast<LbSlot*>(static_cast<char*>(a.ws) + kChainFlagBytes);
-    if ((st = chain_setup(p.geo, v, a.ws, stream))) return st;
-    const void* fn = dyc ? pick_rc<true>(a.dtype, a.causal, true)
-                         : pick_rc<false>(a.dtype, a.causal, true);
-    if ((st = launch(fn, p.geo.nchunks, kChainWaves, p, stream))) return st;
-    p.skip = static_cast<const uint32_t*>(a.ws);
-  } else {
-    p.geo = chain_geo(g, v, nullptr);
-  }
-  p.geo.kr = rc_chunks_per_row(a.T, v);
-  p.geo.nchunks = a.C * p.geo.kr;
+  // the per-item walk first (for chained calls it clears the slots and
+  // takes the unaligned segments), then the chained walk for chunk-aligned
+  // long segments
+  const bool chained =
+      !a.inplace && chain_share(g, true, v, a.ws, a.ws_bytes, true);
+  p.geo = chain_geo(g, v);
+  p.slots = reinterpret_cast<LbSlot*>(g.chain_slots);
+  p.chain_ch = g.chain_ch;
+  p.chain_slots = g.chain_slots;
+  p.chain_words = g.chain_words;
+  p.chain_flag = g.chain_flag;
+  RcParams pi = p;
+  pi.geo.kr = rc_chunks_per_row(a.T, v);
+  pi.geo.nchunks = a.C * pi.geo.kr;
   int64_t blocks = a.S * a.C;
-  if (p.skip != nullptr && blocks > kSkippableWaves / kChainWaves)
+  if (chained && blocks > kSkippableWaves / kChainWaves)
     blocks = kSkippableWaves / kChainWaves;
   const void* fn = dyc ? pick_rc<true>(a.dtype, a.causal, false)
                        : pick_rc<false>(a.dtype, a.causal, false);
-  return launch(fn, blocks, kChainWaves, p, stream);
+  int st = launch(fn, blocks, kChainWaves, pi, stream);
+  if (st || !chained) return st;
+  fn = dyc ? pick_rc<true>(a.dtype, a.causal, true)
+           : pick_rc<false>(a.dtype, a.causal, true);
+  return launch(fn, p.geo.nchunks, kChainWaves, p, stream);
 }
 
 }  // namespace asc

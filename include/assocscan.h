@@ -89,10 +89,11 @@ int64_t asc_scan_workspace_bytes(int64_t num_seq, int64_t num_channels,
  * Which walk a workspace of asc_scan_workspace_bytes() buys for this
  * geometry: 0 = none (the workspace-free walks run), ASC_WALK_LOOKBACK (few
  * items, any cu_seqlens: the tree walk, or the look-back walk for tensors at
- * different 16-byte phases), ASC_WALK_CHAINED (long segments; runs when
- * every edge in cu_seqlens is a multiple of the chunk size -- 4096 fp32 /
- * 8192 fp16-bf16 elements -- checked on the device, else the workspace-free
- * walks run), or a negative ASC_E_* code.  The row-gradient entry points
+ * different 16-byte phases), ASC_WALK_CHAINED (long segments; the chained
+ * walk takes every segment whose edges are both multiples of the chunk size
+ * -- 4096 fp32 / 8192 fp16-bf16 elements -- and the one-wave walk, launched
+ * first in the same call, every other segment; cu_seqlens is read on the
+ * device), or a negative ASC_E_* code.  The row-gradient entry points
  * below cannot use the look-back walk (they take the workspace-free walks
  * instead).  No reference counterpart.
  */
@@ -104,10 +105,12 @@ int asc_scan_workspace_walk(int64_t num_seq, int64_t num_channels,
  * Test hook, no reference counterpart: sets how many times a wave of the
  * look-back, chained or tree walk polls a preceding tile's slot before it
  * gives up waiting: a look-back wave then computes that tile's carry map
- * from the tile's inputs itself; a chained or tree walk's call is redone
- * by a workspace-free walk (0 = give up at once; the default keeps the
- * fallback for pathological scheduling only).  Returns the previous value.  Process-wide (an atomic: safe to call from any host
- * thread); affects launches issued after the call.
+ * from the tile's inputs itself, a chained-walk chunk scans its segment's
+ * prefix from the inputs itself, and a tree walk's call is redone by a
+ * workspace-free walk (0 = give up at once; the default keeps the
+ * fallback for pathological scheduling only).  Returns the previous value.
+ * Process-wide (an atomic: safe to call from any host thread); affects
+ * launches issued after the call.
  */
 unsigned asc_set_lookback_spin_limit(unsigned polls);
 

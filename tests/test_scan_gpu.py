@@ -1005,12 +1005,89 @@ def test_chain_walk_parity_and_reproducible(dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
-def test_chain_walk_unaligned_falls_back(dtype):
-  """Same row width, segment edges off the chunk grid: the device check
-  sends the call to the per-item walks, which must match the oracle."""
+def test_chain_walk_mixed_segments(dtype):
+  """Same row width, some segment edges off the chunk grid: the per-item
+  walk (launched first) takes the segments with an edge off the grid, the
+  chained walk the others, in one call; both must match the oracle."""
   CH = _chunk(dtype)
   _chain_case(dtype, [2 * CH + 5, CH - 5, 3 * CH], 130, rows=[0, 77, 129])
   _chain_case(dtype, [2 * CH, CH, 3 * CH - 1, 1], 130, rows=[0, 129])
+  _chain_case(dtype, [2 * CH + 5, CH - 5, 3 * CH + 1, CH - 1], 130,
+              rows=[0, 129])   # no segment aligned: the chained grid idles
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16],
+                         ids=["f32", "bf16"])
+def test_chain_walk_mixed_with_checkpoint(dtype):
+  """A chunk-aligned segment of 70 chunks (past the 64-chunk checkpoint)
+  between short unaligned ones: the chained walk carries across its
+  checkpoint while the per-item walk takes its neighbours."""
+  CH = _chunk(dtype)
+  _chain_case(dtype, [CH - 3, 3, 70 * CH, CH + 5, CH - 5], 130,
+              rows=[0, 64, 129])
+
+
+@pytest.mark.parametrize("case", ["300-aligned", "300-mixed", "5000-aligned"])
+def test_chain_walk_many_segments(case):
+  """More segments than one wave surveys at once: 300 chunk-aligned ones
+  (the per-item walk's first wave surveys them in two batches: the chained
+  walk reads each chunk before looking it up), 300 with two edges off the
+  grid (per-chunk lookups), 5000 (past what is surveyed: per-chunk lookups
+  and per-item tests)."""
+  CH = 4096
+  if case == "300-aligned":
+    lens, C = [CH * (1 + i % 3) for i in range(300)], 2
+  elif case == "300-mixed":
+    lens, C = [CH * (1 + i % 3) for i in range(300)], 2
+    lens[100] += 9
+    lens[101] -= 9
+  else:
+    lens, C = [CH] * 5000, 1
+  _chain_case(torch.float32, lens, C, rows=range(C))
+
+
+def test_chain_walk_dirty_workspace():
+  """A workspace whose every slot reads as published (as a previous call or
+  unrelated data may leave it): the per-item walk launched first clears the
+  slots, so the chained walk's carries are still right, forward and
+  backward, and the results equal a clean workspace's bit for bit."""
+  from associative_scan_triton import _lib
+  lib = _lib.load()
+  CH = 4096
+  lens, C = [3 * CH, 66 * CH, CH], 130
+  S, T = len(lens), sum(lens)
+  g, x, dy = make(lens, C, torch.float32, glo=0.5, n=3)
+  gd, xd, dyd = g.to(DEV), x.to(DEV), dy.to(DEV)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  code = _lib.dtype_code(gd)
+  assert lib.asc_scan_workspace_walk(S, C, T, code, 1) == _lib.WALK_CHAINED
+  nb = lib.asc_scan_workspace_bytes(S, C, T, code, 1)
+  stream = torch.cuda.current_stream().cuda_stream
+  outs = []
+  for dirty in (False, True):
+    ws = torch.zeros(nb // 8, dtype=torch.int64, device=DEV)
+    if dirty:
+      ws.fill_((2 << 32) | 0x3F800000)   # status "inclusive", value 1.0
+    h, dx, dg = (torch.empty_like(gd) for _ in range(3))
+    assert lib.asc_scan_fwd(gd.data_ptr(), xd.data_ptr(), h.data_ptr(), None,
+                            cu.data_ptr(), 1, S, C, T, code, 0, ws.data_ptr(),
+                            nb, stream) == 0
+    if dirty:
+      ws.fill_((2 << 32) | 0x3F800000)
+    assert lib.asc_scan_bwd(dyd.data_ptr(), gd.data_ptr(), h.data_ptr(),
+                            dx.data_ptr(), dg.data_ptr(), cu.data_ptr(), 1, S,
+                            C, T, code, 1, ws.data_ptr(), nb, stream) == 0
+    torch.cuda.synchronize()
+    outs.append((h, dx, dg))
+  for a, b in zip(*outs):
+    assert torch.equal(a, b)
+  h, dx, dg = outs[1]
+  for r in (0, 129):
+    sl = slice(r, r + 1)
+    check_close(h[sl], oracle_fwd(g[sl], x[sl], lens), torch.float32, "h")
+    dx_ref, dg_ref = oracle_bwd(dy[sl], g[sl], npf(h[sl]), lens, causal=True)
+    check_close(dx[sl], dx_ref, torch.float32, "dx")
+    check_close(dg[sl], dg_ref, torch.float32, "dg")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16],
@@ -1034,12 +1111,15 @@ def test_chain_walk_bounded_wait_fallback():
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16],
                          ids=["f32", "bf16"])
-def test_chain_walk_bidirectional(dtype):
-  """Both branches with chunk-aligned long segments over 130 rows (one
-  chained launch per branch)."""
+@pytest.mark.parametrize("mixed", [False, True], ids=["aligned", "mixed"])
+def test_chain_walk_bidirectional(dtype, mixed):
+  """Both branches with long segments over 130 rows (one chained launch per
+  branch), all chunk-aligned or some with an edge off the chunk grid (those
+  run the per-item walk, both branches in one grid)."""
   from associative_scan_triton import _lib, _ops
   CH = _chunk(dtype)
-  lens, C = [CH, 2 * CH], 130
+  lens = [CH + 3, 2 * CH - 3, 2 * CH] if mixed else [CH, 2 * CH]
+  C = 130
   gf, xf, dyf = make(lens, C, dtype, seed=1, glo=0.5, n=3)
   gb, xb, dyb = make(lens, C, dtype, seed=2, glo=0.5, n=3)
   T = sum(lens)
