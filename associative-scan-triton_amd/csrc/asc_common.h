@@ -660,17 +660,20 @@ __device__ inline uint32_t chain_survey(const void* cu, int cu64, int64_t S,
 
 // Prologue of a per-item walk launched before the chained walk (see
 // Geometry::chain_ch), for wave gw of the grid's nw: clears its share of
-// the chained walk's slots; wave 0 surveys up to kChainSurveyMax segments
-// (a loop of batches) and writes the flag the chained walk reads; returns
-// true when the walk has no item to take (one batch per wave).
+// the chained walk's slots; the waves of the first workgroup survey up to
+// kChainSurveyMax segments (a loop of batches) and its first wave writes
+// the flag the chained walk reads, the others survey one batch.  Returns
+// true when the walk has no item to take (the same value in every wave of
+// a workgroup, so that they all return together).
 constexpr int64_t kChainSurveyMax = 16 * kChainBatch - 1;
 __device__ inline bool chain_prologue(const Geometry& geo, int64_t gw,
                                       int64_t nw, int lane) {
   for (int64_t i = gw * kWave + lane; i < geo.chain_words; i += nw * kWave)
     geo.chain_slots[i] = 0ull;
+  const bool first = blockIdx.x == 0;
   const uint32_t sv =
       chain_survey(geo.cu, geo.cu64, geo.S, geo.T, geo.chain_ch, lane,
-                   gw == 0 ? kChainSurveyMax : kChainBatch - 1);
+                   first ? kChainSurveyMax : kChainBatch - 1);
   if (gw == 0 && lane == 0) *geo.chain_flag = sv;
   return sv == kChainAll;
 }
