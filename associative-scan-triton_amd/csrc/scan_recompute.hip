@@ -574,9 +574,13 @@ int rc_bwd(const RcArgs& a, void* stream) {
   RcParams pi = p;
   pi.geo.kr = rc_chunks_per_row(a.T, v);
   pi.geo.nchunks = a.C * pi.geo.kr;
+  // before the chained walk the grid is capped at 8 workgroups per CU
+  // (grid-stride loops take the rest): where every segment is aligned each
+  // workgroup looks at cu_seqlens once and returns, 2-3 resident at a time
+  // per CU (an uncapped grid of 12288 cost 30-50 us at cfg5)
+  constexpr int64_t kRcPartnerBlocks = 2048;
   int64_t blocks = a.S * a.C;
-  if (chained && blocks > kSkippableWaves / kChainWaves)
-    blocks = kSkippableWaves / kChainWaves;
+  if (chained && blocks > kRcPartnerBlocks) blocks = kRcPartnerBlocks;
   const void* fn = dyc ? pick_rc<true>(a.dtype, a.causal, false)
                        : pick_rc<false>(a.dtype, a.causal, false);
   int st = launch(fn, blocks, kChainWaves, pi, stream);
