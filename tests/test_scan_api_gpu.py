@@ -54,9 +54,13 @@ class _Counter:
     monkeypatch.setattr(_ops, name, wrapped)
 
 
-# lens in chunks: one to three chunks per segment; a segment of 70 chunks
-# (past the 64-chunk checkpoint) beside four one-chunk segments
-GEOMS = {"short": [2, 1, 3], "checkpoint": [70, 1, 1, 1, 1]}
+# segment lengths for a chunk of CH elements: one to three chunks per
+# segment; a segment of 70 chunks (past the 64-chunk checkpoint) beside four
+# one-chunk segments; two segments with an edge off the chunk grid (the
+# one-wave walk takes them) beside a chunk-aligned one
+GEOMS = {"short": lambda CH: [2 * CH, CH, 3 * CH],
+         "checkpoint": lambda CH: [70 * CH, CH, CH, CH, CH],
+         "mixed": lambda CH: [2 * CH + 5, CH - 5, 3 * CH]}
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
@@ -64,7 +68,7 @@ GEOMS = {"short": [2, 1, 3], "checkpoint": [70, 1, 1, 1, 1]}
 @pytest.mark.parametrize("compiled", [False, True], ids=["eager", "compiled"])
 def test_time_constant_gradient_chained(dtype, geom, compiled, monkeypatch):
   C = 130
-  lens = [k * _chunk(dtype) for k in GEOMS[geom]]
+  lens = GEOMS[geom](_chunk(dtype))
   T = sum(lens)
   lib = _lib.load()
   assert lib.asc_scan_workspace_walk(len(lens), C, T, _lib.dtype_code(

@@ -30,6 +30,10 @@ CASES = [
   ("chained", torch.float32, 129, [4096, 2 * 4096], _lib.WALK_CHAINED, 0),
   ("chained-bf16", torch.bfloat16, 300, [8192, 8192], _lib.WALK_CHAINED, 0),
   ("chained-bf16", torch.bfloat16, 200, [8192], _lib.WALK_CHAINED, 0),
+  # edges off the chunk grid: the one-wave walk takes those segments
+  ("chained-mixed", torch.float32, 130, [2 * 4096 + 5, 4096 - 5, 3 * 4096],
+   _lib.WALK_CHAINED, 0),
+  ("chained-mixed", torch.float32, 129, [4096 + 3, 4096 - 3], _lib.WALK_CHAINED, 0),
   ("tree", torch.float32, 5, [300000, 7, 50000], _lib.WALK_LOOKBACK, 0),
   ("tree", torch.float32, 2, [20000, 3], _lib.WALK_LOOKBACK, 0),
   ("tree-bf16", torch.bfloat16, 3, [400000, 9], _lib.WALK_LOOKBACK, 0),
