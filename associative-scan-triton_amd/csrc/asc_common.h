@@ -692,13 +692,9 @@ __device__ inline bool chain_prologue(const Geometry& geo, int64_t gw,
 // the order (the BLK instantiation) from the mean segment length.
 // Otherwise: the same segment of neighbouring channels (channel-major).
 constexpr int64_t kItemChanBlock = 8;
-template <bool CHAIN = false>
-__device__ inline bool item_range(const Geometry& geo, int64_t w, int& br,
-                                  int64_t& P0, int64_t& P1, int64_t& row,
-                                  bool blocks) {
-  br = w >= geo.items ? 1 : 0;
-  const int64_t r = w - br * geo.items;
-  int64_t s, c;
+// Segment s and channel c of item r of a branch (the orders above).
+__device__ inline void item_seg_chan(const Geometry& geo, int64_t r,
+                                     bool blocks, int64_t& s, int64_t& c) {
   if (blocks) {
     // blocks of kItemChanBlock channels; inside a block the same segment of
     // its channels, then the next segment
@@ -719,6 +715,16 @@ __device__ inline bool item_range(const Geometry& geo, int64_t w, int& br,
     s = r / geo.C;
     c = r - s * geo.C;
   }
+}
+
+template <bool CHAIN = false>
+__device__ inline bool item_range(const Geometry& geo, int64_t w, int& br,
+                                  int64_t& P0, int64_t& P1, int64_t& row,
+                                  bool blocks) {
+  br = w >= geo.items ? 1 : 0;
+  const int64_t r = w - br * geo.items;
+  int64_t s, c;
+  item_seg_chan(geo, r, blocks, s, c);
   int64_t t0 = cu_at(geo, s), t1 = cu_at(geo, s + 1);
   if (CHAIN && chain_takes(geo.chain_ch, geo.T, t0, t1)) return false;
   t0 = t0 < 0 ? 0 : (t0 > geo.T ? geo.T : t0);
@@ -937,6 +943,14 @@ bool tree_fwd(const FwdParams& p, int dtype, int dirs, bool aln, void* ws,
 bool tree_bwd(const BwdParams& p, int dtype, int dirs, bool aln, bool dyc,
               void* ws, int64_t ws_bytes, void* stream, int& status,
               const uint32_t** fail);
+
+// scan_pair.hip: two items per wave (one per 32-lane half) for short
+// segments.  pair_use: the geometry's mean segment fits one step of a half
+// (32 vectors); pair_fwd / pair_bwd launch it (16-byte aligned tensors, no
+// gate product; arguments validated).
+bool pair_use(const Geometry& geo, int v);
+int pair_fwd(const FwdParams& p, int dtype, int dirs, void* stream);
+int pair_bwd(const BwdParams& p, int dtype, int dirs, bool dyc, void* stream);
 
 // scan_chain.hip: chained chunks for segments aligned to the chunk size.
 // chain_bytes: its workspace (0 when the geometry cannot use it).

@@ -18,6 +18,11 @@
 constexpr int64_t kScratchBytes = int64_t(8) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
+// Short segments: two items per wave (1) or one (0).
+#ifndef ASC_PAIR_WALK
+#define ASC_PAIR_WALK 1
+#endif
+
 // Few-item problems: the tree walk (1) or the look-back walk (0).
 #ifndef ASC_USE_TREE
 #define ASC_USE_TREE 1
@@ -139,8 +144,12 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
   // (the chained walk's partner is the one-wave walk: its launch costs a
   // few microseconds when it has nothing to do, the workgroup walks' 20-30)
   const int nw = wa || chained ? 0 : pick_walk(S, C, T, nbranch, v, false);
-  st = nw ? wg_fwd(p, nw, dtype, dirs, aln, stream)
-          : item_fwd(p, dtype, dirs, aln, wa, stream);
+  if (nw)
+    st = wg_fwd(p, nw, dtype, dirs, aln, stream);
+  else if (ASC_PAIR_WALK && aln && !wa && !chained && pair_use(p.geo, v))
+    st = pair_fwd(p, dtype, dirs, stream);
+  else
+    st = item_fwd(p, dtype, dirs, aln, wa, stream);
   if (st || !chained) return st;
   return chain_fwd(p, dtype, dirs, stream);
 }
@@ -226,8 +235,12 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
     chained = chain_plan(p.geo, aln, dtype, ws, ws_bytes, true);
   }
   const int nw = chained ? 0 : pick_walk(S, C, T, nbranch, v, true);
-  st = nw ? wg_bwd(p, nw, dtype, dirs, aln, dyc, stream)
-          : item_bwd(p, dtype, dirs, aln, dyc, stream);
+  if (nw)
+    st = wg_bwd(p, nw, dtype, dirs, aln, dyc, stream);
+  else if (ASC_PAIR_WALK && aln && !chained && pair_use(p.geo, v))
+    st = pair_bwd(p, dtype, dirs, dyc, stream);
+  else
+    st = item_bwd(p, dtype, dirs, aln, dyc, stream);
   if (st || !chained) return st;
   return chain_bwd(p, dtype, dyc, dirs, stream);
 }

@@ -1144,6 +1144,94 @@ def test_chain_walk_bidirectional(dtype, mixed):
 
 
 # ---------------------------------------------------------------------------
+# two items per wave, one per 32-lane half (a mean segment of at most 128
+# fp32 / 256 fp16-bf16 elements, 16-byte aligned tensors, no workspace)
+# ---------------------------------------------------------------------------
+
+PAIR_LENS = {
+  "uniform": [128] * 8,
+  # items of several steps of a half beside one-element and empty ones
+  "ragged": [1, 300, 7, 0, 129, 64, 2, 33, 97],
+  "odd": [5, 9, 100],
+}
+
+
+def _pair_geometry(lens, dtype):
+  per_half = 128 if dtype == torch.float32 else 256
+  assert sum(lens) <= len(lens) * per_half
+
+
+@pytest.fixture
+def no_workspace():
+  from associative_scan_triton import _ops
+  prev = _ops.USE_WORKSPACE
+  _ops.USE_WORKSPACE = False
+  yield
+  _ops.USE_WORKSPACE = prev
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("name", sorted(PAIR_LENS))
+@pytest.mark.parametrize("C", [7, 130])
+def test_pair_walk_parity(dtype, name, C, no_workspace):
+  """Forward (both directions) and dense backward (both) against the
+  oracle; an odd number of items leaves the last pair with one item."""
+  from associative_scan_triton import _ops
+  lens = PAIR_LENS[name]
+  _pair_geometry(lens, dtype)
+  g, x, dy = make(lens, C, dtype, glo=0.5, n=3)
+  gd, xd, dyd = g.to(DEV), x.to(DEV), dy.to(DEV)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  for rev in (False, True):
+    h = torch.empty_like(xd)
+    _ops.scan_fwd(gd, xd, h, cu, reverse=rev)
+    check_close(h, oracle_fwd(g, x, lens, reverse=rev), dtype, f"h rev={rev}")
+    dx, dg = torch.empty_like(xd), torch.empty_like(xd)
+    _ops.scan_bwd(dyd, gd, h, dx, dg, cu, causal=not rev)
+    dx_ref, dg_ref = oracle_bwd(dy, g, npf(h), lens, causal=not rev)
+    check_close(dx, dx_ref, dtype, f"dx rev={rev}")
+    check_close(dg, dg_ref, dtype, f"dg rev={rev}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("name", ["ragged", "odd"])
+def test_pair_walk_bidirectional_and_row_gradient(dtype, name, no_workspace):
+  """Both branches in one launch (each pair's two items from one branch),
+  and a gradient constant along time (each half reads its row's value):
+  bits equal to the dense gradient's, values against the oracle."""
+  from associative_scan_triton import _ops
+  lens, C = PAIR_LENS[name], 9
+  _pair_geometry(lens, dtype)
+  gf, xf, dyf = make(lens, C, dtype, seed=1, glo=0.5, n=3)
+  gb, xb, dyb = make(lens, C, dtype, seed=2, glo=0.5, n=3)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  d = [t.to(DEV) for t in (gf, xf, gb, xb, dyf, dyb)]
+  hf, hb = torch.empty_like(d[0]), torch.empty_like(d[0])
+  _ops.scan_bidi_fwd(d[0], d[1], d[2], d[3], hf, hb, cu)
+  check_close(hf, oracle_fwd(gf, xf, lens), dtype, "hf")
+  check_close(hb, oracle_fwd(gb, xb, lens, reverse=True), dtype, "hb")
+  outs = [torch.empty_like(d[0]) for _ in range(4)]
+  _ops.scan_bidi_bwd(d[4], d[5], d[0], d[2], hf, hb, *outs, cu)
+  dxf, dgf = oracle_bwd(dyf, gf, npf(hf), lens, causal=True)
+  dxb, dgb = oracle_bwd(dyb, gb, npf(hb), lens, causal=False)
+  check_close(outs[0], dxf, dtype, "dxf")
+  check_close(outs[1], dgf, dtype, "dgf")
+  check_close(outs[2], dxb, dtype, "dxb")
+  check_close(outs[3], dgb, dtype, "dgb")
+  # one value per row, three elements apart, against the same value dense
+  rows = torch.randn(C, 3, generator=torch.Generator().manual_seed(5)).to(dtype)
+  T = sum(lens)
+  dense = rows[:, 1:2].expand(C, T).contiguous()
+  dx1, dg1, dx2, dg2 = (torch.empty_like(d[0]) for _ in range(4))
+  _ops.scan_bwd_rowgrad(rows.to(DEV)[:, 1], 3, d[0], hf, dx1, dg1, cu, True)
+  _ops.scan_bwd(dense.to(DEV), d[0], hf, dx2, dg2, cu, causal=True)
+  assert torch.equal(dx1, dx2) and torch.equal(dg1, dg2)
+  dx_ref, dg_ref = oracle_bwd(dense, gf, npf(hf), lens, causal=True)
+  check_close(dx1, dx_ref, dtype, "dx (row gradient)")
+  check_close(dg1, dg_ref, dtype, "dg (row gradient)")
+
+
+# ---------------------------------------------------------------------------
 # HIP graph capture
 # ---------------------------------------------------------------------------
 
