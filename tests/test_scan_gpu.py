@@ -1148,17 +1148,22 @@ def test_chain_walk_bidirectional(dtype, mixed):
 # fp32 / 256 fp16-bf16 elements, 16-byte aligned tensors, no workspace)
 # ---------------------------------------------------------------------------
 
+# (means of up to one step of a half, and a few geometries just past it,
+# which run one wave per item)
 PAIR_LENS = {
   "uniform": [128] * 8,
   # items of several steps of a half beside one-element and empty ones
   "ragged": [1, 300, 7, 0, 129, 64, 2, 33, 97],
   "odd": [5, 9, 100],
+  "uniform2": [256] * 6,
+  "ragged2": [1, 700, 150, 0, 255, 257, 3, 400, 33],
+  "uniform2-half": [512] * 5,
 }
 
 
 def _pair_geometry(lens, dtype):
   per_half = 128 if dtype == torch.float32 else 256
-  assert sum(lens) <= len(lens) * per_half
+  assert sum(lens) <= len(lens) * 4 * per_half
 
 
 @pytest.fixture
@@ -1194,7 +1199,7 @@ def test_pair_walk_parity(dtype, name, C, no_workspace):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
-@pytest.mark.parametrize("name", ["ragged", "odd"])
+@pytest.mark.parametrize("name", ["ragged", "odd", "ragged2"])
 def test_pair_walk_bidirectional_and_row_gradient(dtype, name, no_workspace):
   """Both branches in one launch (each pair's two items from one branch),
   and a gradient constant along time (each half reads its row's value):
