@@ -1,0 +1,111 @@
+"""Seeded random geometries through every walk, against the fp64 oracle.
+
+Each case draws a dtype, a row count, segment lengths from a mixture (single
+elements, empty segments, short segments that take two items per wave,
+lengths around the 16-byte vector and the sub-tile, multiples of the
+chained walk's chunk with and without an element off the grid, long
+segments), with and without the workspace, and runs the forward in both
+directions, the backward of each, the two-branch calls and the row-constant
+gradient; sampled rows are compared with the oracle.  The walk a case takes
+follows from its geometry (tree, chained with its one-wave partner, pair,
+one-wave, workgroup), so the draws cover their mixtures as well.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import DEV, check_close, cu_of, make, npf, oracle_bwd, oracle_fwd
+from associative_scan_triton import _ops
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+NCASES = 48
+
+
+def _chunk(dtype):
+  return 4096 if dtype == torch.float32 else 8192
+
+
+def _draw(seed):
+  rng = np.random.default_rng(seed)
+  dtype = DTYPES[rng.integers(3)]
+  CH = _chunk(dtype)
+  kind = rng.choice(["short", "mixed", "chunky", "long"])
+  S = int(rng.integers(1, 24))
+  lens = []
+  for _ in range(S):
+    r = rng.random()
+    if kind == "short":
+      n = int(rng.integers(0, 300)) if r < 0.9 else int(rng.integers(300, 2000))
+    elif kind == "chunky":
+      n = CH * int(rng.integers(1, 4)) + (int(rng.integers(-3, 4)) if r < 0.3 else 0)
+    elif kind == "long":
+      n = int(rng.integers(1, 60000))
+    else:
+      n = int(rng.choice([0, 1, 3, 4, 255, 256, 257, 511, 513, 1000, 4097,
+                          CH, 2 * CH, int(rng.integers(1, 5000))]))
+    lens.append(max(n, 0))
+  if sum(lens) == 0:
+    lens[0] = 1
+  budget = 6_000_000 // sum(lens)
+  C = int(max(1, min(budget, rng.choice([1, 3, 64, 129, 200]))))
+  use_ws = bool(rng.random() < 0.7)
+  return dtype, lens, C, use_ws
+
+
+@pytest.mark.parametrize("seed", range(NCASES))
+def test_random_geometry(seed):
+  dtype, lens, C, use_ws = _draw(seed)
+  T = sum(lens)
+  g, x, dy = make(lens, C, dtype, seed=seed, glo=0.5, n=3)
+  gd, xd, dyd = g.to(DEV), x.to(DEV), dy.to(DEV)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  rows = sorted({0, C // 2, C - 1})
+  prev = _ops.USE_WORKSPACE
+  _ops.USE_WORKSPACE = use_ws
+  try:
+    for rev in (False, True):
+      h = torch.empty_like(xd)
+      _ops.scan_fwd(gd, xd, h, cu, reverse=rev)
+      dx, dg = torch.empty_like(xd), torch.empty_like(xd)
+      _ops.scan_bwd(dyd, gd, h, dx, dg, cu, causal=not rev)
+      torch.cuda.synchronize()
+      for r in rows:
+        sl = slice(r, r + 1)
+        what = f"seed {seed} {dtype} C={C} S={len(lens)} T={T} ws={use_ws} rev={rev} row {r}"
+        check_close(h[sl], oracle_fwd(g[sl], x[sl], lens, reverse=rev), dtype,
+                    "h " + what)
+        dx_ref, dg_ref = oracle_bwd(dy[sl], g[sl], npf(h[sl]), lens,
+                                    causal=not rev)
+        check_close(dx[sl], dx_ref, dtype, "dx " + what)
+        check_close(dg[sl], dg_ref, dtype, "dg " + what)
+    # both branches in one call, and the gradient of out.sum() (one value
+    # per row) against the same gradient materialised
+    hf, hb = torch.empty_like(xd), torch.empty_like(xd)
+    _ops.scan_bidi_fwd(gd, xd, gd, dyd, hf, hb, cu)
+    outs = [torch.empty_like(xd) for _ in range(4)]
+    _ops.scan_bidi_bwd(dyd, xd, gd, gd, hf, hb, *outs, cu)
+    ones = torch.ones(C, dtype=dtype, device=DEV)
+    dx1, dg1, dx2, dg2 = (torch.empty_like(xd) for _ in range(4))
+    _ops.scan_bwd_rowgrad(ones, 1, gd, hf, dx1, dg1, cu, True)
+    _ops.scan_bwd(torch.ones_like(xd), gd, hf, dx2, dg2, cu, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(dx1, dx2) and torch.equal(dg1, dg2), f"seed {seed}"
+    for r in rows:
+      sl = slice(r, r + 1)
+      what = f"seed {seed} two-branch row {r}"
+      check_close(hf[sl], oracle_fwd(g[sl], x[sl], lens), dtype, "hf " + what)
+      check_close(hb[sl], oracle_fwd(g[sl], dy[sl], lens, reverse=True), dtype,
+                  "hb " + what)
+      dxf, dgf = oracle_bwd(dy[sl], g[sl], npf(hf[sl]), lens, causal=True)
+      dxb, dgb = oracle_bwd(x[sl], g[sl], npf(hb[sl]), lens, causal=False)
+      check_close(outs[0][sl], dxf, dtype, "dxf " + what)
+      check_close(outs[1][sl], dgf, dtype, "dgf " + what)
+      check_close(outs[2][sl], dxb, dtype, "dxb " + what)
+      check_close(outs[3][sl], dgb, dtype, "dgb " + what)
+  finally:
+    _ops.USE_WORKSPACE = prev
