@@ -128,12 +128,13 @@ __device__ inline void pair_bwd(const BwdPtrs& t, const HalfItem& it, int hl,
     const int64_t vi = RB ? it.v1 - i : it.v0 + i;
     const int64_t pv = vi * V;
     float g[V], dy[V], h[V];
-    if (DYC)
-      dyc_vec<IO, true>(dyv, vi, ok, it.P0, it.P1, dy);
-    else
+    // (DYC: the row value fills dy after the loads are issued, so that its
+    // own load does not hold them back)
+    if (!DYC)
       load_vec<IO, true, true, true>(t.dy, vi, ok, it.P0, it.P1, 0.0f, dy, t.pend);
     load_vec<IO, true, true, true>(t.g, vi, ok, it.P0, it.P1, 1.0f, g, t.pend);
     load_vec<IO, true, true, true>(t.h, vi, ok, it.P0, it.P1, 0.0f, h, t.pend);
+    if (DYC) dyc_vec<IO, true>(dyv, vi, ok, it.P0, it.P1, dy);
     // the state just past this step in B order (0 past the item)
     const int64_t il = k * kHalf + kHalf - 1;
     const int64_t vl = RB ? it.v1 - il : it.v0 + il;
