@@ -114,7 +114,23 @@ __device__ inline uint32_t f2b(float f) {
   return __builtin_bit_cast(unsigned short, static_cast<__bf16>(f));
 }
 
-template <float (*CVT)(uint32_t), uint32_t (*RND)(float)>
+// Two elements rounded into one word (lo in bits 0-15) by one packed
+// conversion (v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32, round-to-nearest-even
+// like the scalar ones above).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t f2h2(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+__device__ inline uint32_t f2b2(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+template <float (*CVT)(uint32_t), uint32_t (*RND)(float),
+          uint32_t (*RND2)(float, float)>
 struct IoHalf {
   static constexpr int V = 8;
   static constexpr int ES = 2;
@@ -129,7 +145,7 @@ struct IoHalf {
   __device__ static inline uint4 pack(const float* f) {
     uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = RND(f[2 * i]) | (RND(f[2 * i + 1]) << 16);
+    for (int i = 0; i < 4; ++i) w[i] = RND2(f[2 * i], f[2 * i + 1]);
     return make_uint4(w[0], w[1], w[2], w[3]);
   }
   __device__ static inline float load1(const char* p) {
@@ -140,8 +156,8 @@ struct IoHalf {
   }
   __device__ static inline uint32_t bits(float v) { return RND(v); }
 };
-using IoF16 = IoHalf<h2f, f2h>;
-using IoBF16 = IoHalf<b2f, f2b>;
+using IoF16 = IoHalf<h2f, f2h, f2h2>;
+using IoBF16 = IoHalf<b2f, f2b, f2b2>;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -186,8 +202,42 @@ __device__ inline void affine_step(float& a, float& x) {
   a = a * as;
 }
 
+template <int CTRL, int ROWMASK>
+__device__ inline void mul_step(float& p) {
+  p = p * dpp<CTRL, ROWMASK>(1.0f, p);
+}
+
+// The lane scans below put the DPP source on the arithmetic itself
+// (v_fmac_f32_dpp x, x, a: x = x[src] * a + x; v_mul_f32_dpp a, a, a:
+// a = a[src] * a).  Without bound_ctrl a lane whose source is out of its row,
+// or whose row is masked off, is not written, which is the identity; the
+// builtin form above spends a v_mov of the identity and a v_mov_b32_dpp per
+// operand and step on the same thing.  A VALU result read as a DPP source
+// needs two wait states: each block starts and ends with s_nop 1 for the
+// code around it, and within a block the other operation of the step and an
+// s_nop 0 separate a write from its DPP read.
+#ifndef ASC_DPP_ASM
+#define ASC_DPP_ASM 1
+#endif
+#define ASC_DPP_SHR(n) "row_shr:" #n " row_mask:0xf bank_mask:0xf"
+#define ASC_DPP_BC15 "row_bcast:15 row_mask:0xa bank_mask:0xf"
+#define ASC_DPP_BC31 "row_bcast:31 row_mask:0xc bank_mask:0xf"
+#define ASC_AFFINE(c) \
+  "v_fmac_f32_dpp %1, %1, %0 " c "\n\tv_mul_f32_dpp %0, %0, %0 " c "\n\t"
+#define ASC_MUL(c) "v_mul_f32_dpp %0, %0, %0 " c "\n\ts_nop 1\n\t"
+#define ASC_AFFINE_ROWS                                              \
+  "s_nop 1\n\t" ASC_AFFINE(ASC_DPP_SHR(1)) "s_nop 0\n\t"            \
+      ASC_AFFINE(ASC_DPP_SHR(2)) "s_nop 0\n\t" ASC_AFFINE(ASC_DPP_SHR(4)) \
+          "s_nop 0\n\t" ASC_AFFINE(ASC_DPP_SHR(8)) "s_nop 0\n\t"        \
+              ASC_AFFINE(ASC_DPP_BC15)
+
 // Inclusive scan of affine maps over the 64 lanes (lane 0 first).
 __device__ inline void wave_scan_affine(float& a, float& x) {
+  if (ASC_DPP_ASM) {
+    asm(ASC_AFFINE_ROWS "s_nop 0\n\t" ASC_AFFINE(ASC_DPP_BC31) "s_nop 1"
+        : "+v"(a), "+v"(x));
+    return;
+  }
   affine_step<kRowShr1, 0xf>(a, x);
   affine_step<kRowShr2, 0xf>(a, x);
   affine_step<kRowShr4, 0xf>(a, x);
@@ -196,13 +246,29 @@ __device__ inline void wave_scan_affine(float& a, float& x) {
   affine_step<kRowBcast31, 0xc>(a, x);
 }
 
-template <int CTRL, int ROWMASK>
-__device__ inline void mul_step(float& p) {
-  p = p * dpp<CTRL, ROWMASK>(1.0f, p);
+// Inclusive scan of affine maps within each 32-lane half (rows 0-1 and
+// 2-3): the scan above without its last step.
+__device__ inline void half_scan_affine(float& a, float& x) {
+  if (ASC_DPP_ASM) {
+    asm(ASC_AFFINE_ROWS "s_nop 1" : "+v"(a), "+v"(x));
+    return;
+  }
+  affine_step<kRowShr1, 0xf>(a, x);
+  affine_step<kRowShr2, 0xf>(a, x);
+  affine_step<kRowShr4, 0xf>(a, x);
+  affine_step<kRowShr8, 0xf>(a, x);
+  affine_step<kRowBcast15, 0xa>(a, x);
 }
 
 // Inclusive product scan over the 64 lanes.
 __device__ inline void wave_scan_mul(float& p) {
+  if (ASC_DPP_ASM) {
+    asm("s_nop 1\n\t" ASC_MUL(ASC_DPP_SHR(1)) ASC_MUL(ASC_DPP_SHR(2))
+            ASC_MUL(ASC_DPP_SHR(4)) ASC_MUL(ASC_DPP_SHR(8))
+                ASC_MUL(ASC_DPP_BC15) ASC_MUL(ASC_DPP_BC31)
+        : "+v"(p));
+    return;
+  }
   mul_step<kRowShr1, 0xf>(p);
   mul_step<kRowShr2, 0xf>(p);
   mul_step<kRowShr4, 0xf>(p);

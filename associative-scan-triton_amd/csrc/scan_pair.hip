@@ -17,15 +17,6 @@ namespace {
 
 constexpr int kHalf = 32;
 
-// Inclusive affine scan within each 32-lane half (rows 0-1 and 2-3).
-__device__ inline void half_scan_affine(float& a, float& x) {
-  affine_step<kRowShr1, 0xf>(a, x);
-  affine_step<kRowShr2, 0xf>(a, x);
-  affine_step<kRowShr4, 0xf>(a, x);
-  affine_step<kRowShr8, 0xf>(a, x);
-  affine_step<kRowBcast15, 0xa>(a, x);
-}
-
 // The half's value at its last lane (31 or 63).
 __device__ inline float half_last(float v, bool upper) {
   const float lo = readlane(v, kHalf - 1), hi = readlane(v, kWave - 1);
