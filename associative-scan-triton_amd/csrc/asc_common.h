@@ -456,10 +456,11 @@ struct SubScan {
 // g, x in memory order (masked to the identity when MASKED); phead is the
 // segment's first element in scan order (reset exactly there).
 template <class IO, bool REV, bool MASKED>
-__device__ inline SubScan fwd_local(const float* g, const float* x, int64_t pv,
-                                    int64_t phead) {
+__device__ inline void fwd_lanes(const float* g, const float* x, int64_t pv,
+                                 int64_t phead, float& A, float& X) {
   constexpr int V = IO::V;
-  float A = 1.0f, X = 0.0f;
+  A = 1.0f;
+  X = 0.0f;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int j = mem_idx<V, REV>(i);
@@ -475,6 +476,11 @@ __device__ inline SubScan fwd_local(const float* g, const float* x, int64_t pv,
     }
   }
   wave_scan_affine(A, X);
+}
+
+// The lane's exclusive prefix and the sub-tile total from the inclusive
+// lane scan (A, X).
+__device__ inline SubScan sub_scan(float A, float X) {
   SubScan r;
   r.ta = readlane(A, kWave - 1);
   r.tx = readlane(X, kWave - 1);
@@ -483,14 +489,33 @@ __device__ inline SubScan fwd_local(const float* g, const float* x, int64_t pv,
   return r;
 }
 
-// Second phase: the lane re-walks its elements from its prefix applied to
-// the carry into the sub-tile; h in memory order.
 template <class IO, bool REV, bool MASKED>
-__device__ inline void fwd_apply(const float* g, const float* x, int64_t pv,
-                                 int64_t phead, const SubScan& s, float carry,
-                                 float* hout) {
+__device__ inline SubScan fwd_local(const float* g, const float* x, int64_t pv,
+                                    int64_t phead) {
+  float A, X;
+  fwd_lanes<IO, REV, MASKED>(g, x, pv, phead, A, X);
+  return sub_scan(A, X);
+}
+
+// With the carry into the sub-tile already known: y = the lane's inclusive
+// map applied to the carry; lane l starts from y of lane l-1 (lane 0 from
+// the carry) and the carry out is y of lane 63.  The same fmas as applying
+// the exclusive prefix and the total to the carry (lane 0 takes the carry
+// itself, where fma(1, carry, 0) turns a -0 carry into +0), in three VALU
+// operations and one readlane instead of six and two.
+__device__ inline float carried_start(float A, float X, float& carry) {
+  const float y = fmaf(A, carry, X);
+  const float start = dpp<kWaveShr1, 0xf>(carry, y);
+  carry = readlane(y, kWave - 1);
+  return start;
+}
+
+// Second phase: the lane re-walks its elements from its start value hh
+// (its prefix applied to the carry into the sub-tile); h in memory order.
+template <class IO, bool REV, bool MASKED>
+__device__ inline void fwd_walk(const float* g, const float* x, int64_t pv,
+                                int64_t phead, float hh, float* hout) {
   constexpr int V = IO::V;
-  float hh = fmaf(s.ea, carry, s.ex);
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int j = mem_idx<V, REV>(i);
@@ -502,6 +527,13 @@ __device__ inline void fwd_apply(const float* g, const float* x, int64_t pv,
   }
 }
 
+template <class IO, bool REV, bool MASKED>
+__device__ inline void fwd_apply(const float* g, const float* x, int64_t pv,
+                                 int64_t phead, const SubScan& s, float carry,
+                                 float* hout) {
+  fwd_walk<IO, REV, MASKED>(g, x, pv, phead, fmaf(s.ea, carry, s.ex), hout);
+}
+
 // One sub-tile with a carry in a register; writes h (and the gate product
 // when WA) in memory order.
 template <class IO, bool REV, bool MASKED, bool WA>
@@ -509,9 +541,9 @@ __device__ inline void fwd_subtile(const float* g, const float* x, int64_t pv,
                                    int64_t phead, float& carry, float& carry_a,
                                    float* hout, float* aout) {
   constexpr int V = IO::V;
-  const SubScan s = fwd_local<IO, REV, MASKED>(g, x, pv, phead);
-  fwd_apply<IO, REV, MASKED>(g, x, pv, phead, s, carry, hout);
-  carry = fmaf(s.ta, carry, s.tx);
+  float A, X;
+  fwd_lanes<IO, REV, MASKED>(g, x, pv, phead, A, X);
+  fwd_walk<IO, REV, MASKED>(g, x, pv, phead, carried_start(A, X, carry), hout);
   if (WA) {
     float p = 1.0f;
 #pragma unroll
@@ -548,13 +580,14 @@ struct BwdPtrs {
 // just before the sub-tile in B order (it shifts into lane 0); returns the
 // lane's shifted gate for its first element in gprev.
 template <class IO, bool RB, bool MASKED>
-__device__ inline SubScan bwd_local(const float* g, const float* dy, int64_t pv,
-                                    int64_t phead, float carry_g,
-                                    float& gprev) {
+__device__ inline void bwd_lanes(const float* g, const float* dy, int64_t pv,
+                                 int64_t phead, float carry_g, float& gprev,
+                                 float& A, float& X) {
   constexpr int V = IO::V;
   constexpr int jl = mem_idx<V, RB>(V - 1);  // last element in B order
   gprev = dpp<kWaveShr1, 0xf>(carry_g, g[jl]);
-  float A = 1.0f, X = 0.0f;
+  A = 1.0f;
+  X = 0.0f;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int j = mem_idx<V, RB>(i);
@@ -571,12 +604,15 @@ __device__ inline SubScan bwd_local(const float* g, const float* dy, int64_t pv,
     }
   }
   wave_scan_affine(A, X);
-  SubScan r;
-  r.ta = readlane(A, kWave - 1);
-  r.tx = readlane(X, kWave - 1);
-  r.ea = dpp<kWaveShr1, 0xf>(1.0f, A);
-  r.ex = dpp<kWaveShr1, 0xf>(0.0f, X);
-  return r;
+}
+
+template <class IO, bool RB, bool MASKED>
+__device__ inline SubScan bwd_local(const float* g, const float* dy, int64_t pv,
+                                    int64_t phead, float carry_g,
+                                    float& gprev) {
+  float A, X;
+  bwd_lanes<IO, RB, MASKED>(g, dy, pv, phead, carry_g, gprev, A, X);
+  return sub_scan(A, X);
 }
 
 // Second phase: dx by re-walking from the prefix, dg = shifted state * dx.
@@ -584,15 +620,13 @@ __device__ inline SubScan bwd_local(const float* g, const float* dy, int64_t pv,
 // (it shifts into lane 63); ptail is the segment's last element in B order,
 // whose shifted state is the pad 0.
 template <class IO, bool RB, bool MASKED>
-__device__ inline void bwd_apply(const float* g, const float* dy,
-                                 const float* h, int64_t pv, int64_t phead,
-                                 int64_t ptail, float gprev, float hnext_in,
-                                 const SubScan& s, float carry, float* dxo,
-                                 float* dgo) {
+__device__ inline void bwd_walk(const float* g, const float* dy,
+                                const float* h, int64_t pv, int64_t phead,
+                                int64_t ptail, float gprev, float hnext_in,
+                                float d, float* dxo, float* dgo) {
   constexpr int V = IO::V;
   constexpr int jf = mem_idx<V, RB>(0);  // first element in B order
   const float hnx = dpp<kWaveShl1, 0xf>(hnext_in, h[jf]);
-  float d = fmaf(s.ea, carry, s.ex);
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int j = mem_idx<V, RB>(i);
@@ -609,17 +643,26 @@ __device__ inline void bwd_apply(const float* g, const float* dy,
 }
 
 template <class IO, bool RB, bool MASKED>
+__device__ inline void bwd_apply(const float* g, const float* dy,
+                                 const float* h, int64_t pv, int64_t phead,
+                                 int64_t ptail, float gprev, float hnext_in,
+                                 const SubScan& s, float carry, float* dxo,
+                                 float* dgo) {
+  bwd_walk<IO, RB, MASKED>(g, dy, h, pv, phead, ptail, gprev, hnext_in,
+                           fmaf(s.ea, carry, s.ex), dxo, dgo);
+}
+
+template <class IO, bool RB, bool MASKED>
 __device__ inline void bwd_subtile(const float* g, const float* dy,
                                    const float* h, int64_t pv, int64_t phead,
                                    int64_t ptail, float& carry,
                                    float& carry_g, float hnext_in,
                                    float* dxo, float* dgo) {
   constexpr int V = IO::V;
-  float gprev;
-  const SubScan s = bwd_local<IO, RB, MASKED>(g, dy, pv, phead, carry_g, gprev);
-  bwd_apply<IO, RB, MASKED>(g, dy, h, pv, phead, ptail, gprev, hnext_in, s,
-                            carry, dxo, dgo);
-  carry = fmaf(s.ta, carry, s.tx);
+  float gprev, A, X;
+  bwd_lanes<IO, RB, MASKED>(g, dy, pv, phead, carry_g, gprev, A, X);
+  bwd_walk<IO, RB, MASKED>(g, dy, h, pv, phead, ptail, gprev, hnext_in,
+                           carried_start(A, X, carry), dxo, dgo);
   carry_g = readlane(g[mem_idx<V, RB>(V - 1)], kWave - 1);
 }
 

@@ -23,19 +23,17 @@ __device__ inline float half_last(float v, bool upper) {
   return upper ? hi : lo;
 }
 
-// Exclusive prefix of the lane within its half and the half's total.
-__device__ inline SubScan half_finish(float A, float X, int hl, bool upper) {
+// The lane's start value from its half's carry (carried_start within each
+// half: lane 0 of a half takes the carry, not lane 31's value) and the
+// half's carry out.
+__device__ inline float half_carried_start(float A, float X, int hl,
+                                           bool upper, float& carry) {
   half_scan_affine(A, X);
-  SubScan r;
-  r.ta = half_last(A, upper);
-  r.tx = half_last(X, upper);
-  r.ea = dpp<kWaveShr1, 0xf>(1.0f, A);
-  r.ex = dpp<kWaveShr1, 0xf>(0.0f, X);
-  if (hl == 0) {
-    r.ea = 1.0f;
-    r.ex = 0.0f;
-  }
-  return r;
+  const float y = fmaf(A, carry, X);
+  float start = dpp<kWaveShr1, 0xf>(carry, y);
+  if (hl == 0) start = carry;
+  carry = half_last(y, upper);
+  return start;
 }
 
 // Vectors of a half's item in scan order: vector i is v0 + i (forward) or
@@ -85,9 +83,8 @@ __device__ inline void pair_fwd(const FwdPtrs& t, const HalfItem& it, int hl,
         A = A * g[j];
       }
     }
-    const SubScan s = half_finish(A, X, hl, upper);
     float h[V];
-    float hh = fmaf(s.ea, carry, s.ex);
+    float hh = half_carried_start(A, X, hl, upper, carry);
 #pragma unroll
     for (int e = 0; e < V; ++e) {
       const int j = mem_idx<V, REV>(e);
@@ -95,7 +92,6 @@ __device__ inline void pair_fwd(const FwdPtrs& t, const HalfItem& it, int hl,
       h[j] = hh;
     }
     store_vec<IO, true, true>(t.h, vi, ok, it.P0, it.P1, h);
-    carry = fmaf(s.ta, carry, s.tx);
   }
 }
 
@@ -149,13 +145,12 @@ __device__ inline void pair_bwd(const BwdPtrs& t, const HalfItem& it, int hl,
         A = A * gs;
       }
     }
-    const SubScan s = half_finish(A, X, hl, upper);
+    float d = half_carried_start(A, X, hl, upper, carry);
     // second phase: dx, and dg from the shifted state (lane 31 of each
     // half takes its half's halo)
     float hnx = dpp<kWaveShl1, 0xf>(halo, h[jf]);
     if (hl == kHalf - 1) hnx = halo;
     float dx[V], dg[V];
-    float d = fmaf(s.ea, carry, s.ex);
 #pragma unroll
     for (int e = 0; e < V; ++e) {
       const int j = mem_idx<V, RB>(e);
@@ -168,7 +163,6 @@ __device__ inline void pair_bwd(const BwdPtrs& t, const HalfItem& it, int hl,
     }
     store_vec<IO, true, true>(t.dx, vi, ok, it.P0, it.P1, dx);
     store_vec<IO, true, true>(t.dg, vi, ok, it.P0, it.P1, dg);
-    carry = fmaf(s.ta, carry, s.tx);
     carry_g = half_last(g[jl], upper);
   }
 }
