@@ -1158,6 +1158,10 @@ PAIR_LENS = {
   "uniform2": [256] * 6,
   "ragged2": [1, 700, 150, 0, 255, 257, 3, 400, 33],
   "uniform2-half": [512] * 5,
+  # means within a quarter's step (16 lanes x 1 vector: 64 fp32 / 128
+  # fp16-bf16 elements): four items per wave, some of them absent or empty
+  "quad": [64] * 8,
+  "quad-ragged": [1, 40, 64, 0, 17, 63, 2, 130, 9],
 }
 
 
@@ -1199,7 +1203,7 @@ def test_pair_walk_parity(dtype, name, C, no_workspace):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
-@pytest.mark.parametrize("name", ["ragged", "odd", "ragged2"])
+@pytest.mark.parametrize("name", ["ragged", "odd", "ragged2", "quad-ragged"])
 def test_pair_walk_bidirectional_and_row_gradient(dtype, name, no_workspace):
   """Both branches in one launch (each pair's two items from one branch),
   and a gradient constant along time (each half reads its row's value):
