@@ -717,6 +717,26 @@ __device__ inline int64_t cu_at(const Geometry& geo, int64_t i) {
                      : static_cast<int64_t>(reinterpret_cast<const int32_t*>(geo.cu)[i]));
 }
 
+// Both edges of segment s.  The two loads are issued before either value
+// is used: two cu_at calls each wait for their load (the value is moved to
+// a scalar register at once), which put two memory round trips in front of
+// every item's first data load.
+__device__ inline void cu_edges(const Geometry& geo, int64_t s, int64_t& t0,
+                                int64_t& t1) {
+  int64_t a, b;
+  if (geo.cu64) {
+    const int64_t* p = reinterpret_cast<const int64_t*>(geo.cu) + s;
+    a = p[0];
+    b = p[1];
+  } else {
+    const int32_t* p = reinterpret_cast<const int32_t*>(geo.cu) + s;
+    a = p[0];
+    b = p[1];
+  }
+  t0 = uniform(a);
+  t1 = uniform(b);
+}
+
 // Segments the chained walk takes when it runs after a per-item walk (see
 // Geometry::chain_ch): non-empty, inside [0, T], both edges on the chunk
 // grid of ch elements (a power of two; raw cu_seqlens values;
@@ -834,7 +854,8 @@ __device__ inline bool item_range(const Geometry& geo, int64_t w, int& br,
   const int64_t r = w - br * geo.items;
   int64_t s, c;
   item_seg_chan(geo, r, blocks, s, c);
-  int64_t t0 = cu_at(geo, s), t1 = cu_at(geo, s + 1);
+  int64_t t0, t1;
+  cu_edges(geo, s, t0, t1);
   if (CHAIN && chain_takes(geo.chain_ch, geo.T, t0, t1)) return false;
   t0 = t0 < 0 ? 0 : (t0 > geo.T ? geo.T : t0);
   t1 = t1 < t0 ? t0 : (t1 > geo.T ? geo.T : t1);

@@ -274,8 +274,7 @@ __device__ inline void group_items(const Geometry& geo, int64_t w, int& br,
       t0[j] = t0[j > 0 ? j - 1 : 0];
       t1[j] = t1[j > 0 ? j - 1 : 0];
     } else {
-      t0[j] = cu_at(geo, s[j]);
-      t1[j] = cu_at(geo, s[j] + 1);
+      cu_edges(geo, s[j], t0[j], t1[j]);
     }
   }
   P0 = 0;
