@@ -396,6 +396,43 @@ __device__ inline void load_vec(const char* origin, int64_t vi, bool lane_ok,
   }
 }
 
+// One vector of N tensors (same index), masked as load_vec<IO, true, true,
+// true>.  load_vec masks each vector as soon as it is read, so the wave
+// waits for one tensor's load before it issues the next one's; here every
+// load is issued first and the masks follow.  Vectors that need element
+// loads (the tensor's own first and last vectors) take load_vec, for the
+// whole wave when any of its lanes has one.
+template <class IO, int N>
+__device__ inline void load_vecs(const char* const (&origin)[N], int64_t vi,
+                                 bool lane_ok, int64_t P0, int64_t P1,
+                                 const float (&ident)[N],
+                                 float (&f)[N][IO::V], int64_t pend) {
+  constexpr int V = IO::V;
+  const int64_t pv = vi * V;
+  const bool touch = lane_ok && pv + V > P0 && pv < P1;
+  const bool wide = vi >= 1 && pv + V <= pend;
+  if (__builtin_amdgcn_ballot_w64(touch && !wide) != 0) {
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+      load_vec<IO, true, true, true>(origin[n], vi, lane_ok, P0, P1, ident[n],
+                                     f[n], pend);
+    return;
+  }
+  uint4 q[N];
+  if (touch) {
+#pragma unroll
+    for (int n = 0; n < N; ++n) q[n] = ld16(origin[n] + vi * 16);
+  }
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    float v[V];
+    IO::unpack(q[n], v);
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+      f[n][j] = touch && pv + j >= P0 && pv + j < P1 ? v[j] : ident[n];
+  }
+}
+
 // dy of a gradient that is constant along time: value v for the elements
 // inside [P0, P1) (of a valid lane), 0 (the identity) elsewhere.
 template <class IO, bool MASKED>

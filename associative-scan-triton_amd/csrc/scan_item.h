@@ -21,6 +21,18 @@ namespace {
 // the chained walk, which takes segments of a chunk or more.
 constexpr int kFwdDeep = 4, kBwdDeep = 2, kFwdShallow = 2, kBwdShallow = 1;
 
+// BATCH: the masked loads of a sub-tile go through load_vecs (all tensors'
+// loads issued before any is masked): ragged fp32 segments of 16-600
+// elements 65.5 / 99.1 -> 54.0 / 81.9 us fwd / bwd, bf16 segments of
+// 300-1200 elements 96.1 / 162.1 -> 69.5 / 124.2, bf16 segments of 2047
+// 48.3 / 85.8 -> 40.8 / 72.6 (C = 1024-1536, caches flushed).  Not in the
+// deep fp16/bf16 backward: its 113-124 VGPRs leave no room (cfg3 backward
+// 451 -> 464 us with it).
+template <class IO, bool SHALLOW>
+constexpr bool batch_masked_bwd() {
+  return IO::V == 4 || SHALLOW;
+}
+
 template <class IO, bool REV, bool ALN, bool WA, bool MASKED, int NS>
 __device__ inline void fwd_block(const FwdPtrs& t, const Walk<IO, REV>& w,
                                  int64_t k0, int lane, float& carry,
@@ -31,8 +43,20 @@ __device__ inline void fwd_block(const FwdPtrs& t, const Walk<IO, REV>& w,
   for (int u = 0; u < NS; ++u) {
     const int64_t vi = w.vec(k0 + u, lane);
     const bool ok = !MASKED || w.lane_valid(k0 + u, lane);
-    load_vec<IO, ALN, MASKED, true>(t.g, vi, ok, w.P0, w.P1, 1.0f, g[u], w.pend);
-    load_vec<IO, ALN, MASKED, true>(t.x, vi, ok, w.P0, w.P1, 0.0f, x[u], w.pend);
+    if (ALN && MASKED) {
+      const char* const src[2] = {t.g, t.x};
+      const float ident[2] = {1.0f, 0.0f};
+      float gx[2][V];
+      load_vecs<IO, 2>(src, vi, ok, w.P0, w.P1, ident, gx, w.pend);
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        g[u][e] = gx[0][e];
+        x[u][e] = gx[1][e];
+      }
+    } else {
+      load_vec<IO, ALN, MASKED, true>(t.g, vi, ok, w.P0, w.P1, 1.0f, g[u], w.pend);
+      load_vec<IO, ALN, MASKED, true>(t.x, vi, ok, w.P0, w.P1, 0.0f, x[u], w.pend);
+    }
   }
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
@@ -121,7 +145,8 @@ __device__ void fwd_item(const FwdPtrs& t, int64_t P0, int64_t P1, int lane) {
 
 
 // DYC: the gradient is the constant dyv along the item (dy is not read).
-template <class IO, bool RB, bool ALN, bool MASKED, int NS, bool DYC>
+template <class IO, bool RB, bool ALN, bool MASKED, int NS, bool DYC,
+          bool BATCH = true>
 __device__ inline void bwd_block(const BwdPtrs& t, const Walk<IO, RB>& w,
                                  int64_t k0, int lane, float& carry,
                                  float& carry_g, float dyv) {
@@ -131,12 +156,36 @@ __device__ inline void bwd_block(const BwdPtrs& t, const Walk<IO, RB>& w,
   for (int u = 0; u < NS; ++u) {
     const int64_t vi = w.vec(k0 + u, lane);
     const bool ok = !MASKED || w.lane_valid(k0 + u, lane);
-    if (DYC)
+    if (ALN && MASKED && BATCH && !DYC) {
+      const char* const src[3] = {t.dy, t.g, t.h};
+      const float ident[3] = {0.0f, 1.0f, 0.0f};
+      float ygh[3][V];
+      load_vecs<IO, 3>(src, vi, ok, w.P0, w.P1, ident, ygh, w.pend);
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        dy[u][e] = ygh[0][e];
+        g[u][e] = ygh[1][e];
+        h[u][e] = ygh[2][e];
+      }
+    } else if (ALN && MASKED && BATCH) {
+      const char* const src[2] = {t.g, t.h};
+      const float ident[2] = {1.0f, 0.0f};
+      float gh[2][V];
+      load_vecs<IO, 2>(src, vi, ok, w.P0, w.P1, ident, gh, w.pend);
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        g[u][e] = gh[0][e];
+        h[u][e] = gh[1][e];
+      }
       dyc_vec<IO, MASKED>(dyv, vi, ok, w.P0, w.P1, dy[u]);
-    else
-      load_vec<IO, ALN, MASKED, true>(t.dy, vi, ok, w.P0, w.P1, 0.0f, dy[u], w.pend);
-    load_vec<IO, ALN, MASKED, true>(t.g, vi, ok, w.P0, w.P1, 1.0f, g[u], w.pend);
-    load_vec<IO, ALN, MASKED, true>(t.h, vi, ok, w.P0, w.P1, 0.0f, h[u], w.pend);
+    } else {
+      if (DYC)
+        dyc_vec<IO, MASKED>(dyv, vi, ok, w.P0, w.P1, dy[u]);
+      else
+        load_vec<IO, ALN, MASKED, true>(t.dy, vi, ok, w.P0, w.P1, 0.0f, dy[u], w.pend);
+      load_vec<IO, ALN, MASKED, true>(t.g, vi, ok, w.P0, w.P1, 1.0f, g[u], w.pend);
+      load_vec<IO, ALN, MASKED, true>(t.h, vi, ok, w.P0, w.P1, 0.0f, h[u], w.pend);
+    }
   }
   // state just past this block in B order (pad 0 outside the segment)
   float halo = 0.0f;
@@ -229,7 +278,8 @@ __device__ void bwd_item(const BwdPtrs& t, int64_t P0, int64_t P1, int lane,
                          float dyv) {
   const Walk<IO, RB> w(P0, P1, t.pend);
   float carry = 0.0f, carry_g = 1.0f;
-  bwd_block<IO, RB, ALN, true, 1, DYC>(t, w, 0, lane, carry, carry_g, dyv);
+  constexpr bool B = batch_masked_bwd<IO, U == kBwdShallow>();
+  bwd_block<IO, RB, ALN, true, 1, DYC, B>(t, w, 0, lane, carry, carry_g, dyv);
   int64_t k = 1;
   if (ALN) {
     const int64_t nfull = (w.kfast - 1) / U * U;
@@ -244,7 +294,7 @@ __device__ void bwd_item(const BwdPtrs& t, int64_t P0, int64_t P1, int lane,
   for (; k < w.kfast; ++k)
     bwd_block<IO, RB, ALN, false, 1, DYC>(t, w, k, lane, carry, carry_g, dyv);
   for (; k < w.nsub; ++k)
-    bwd_block<IO, RB, ALN, true, 1, DYC>(t, w, k, lane, carry, carry_g, dyv);
+    bwd_block<IO, RB, ALN, true, 1, DYC, B>(t, w, k, lane, carry, carry_g, dyv);
 }
 
 // U: sub-tiles per pipelined block (deep for long items; shallow for short

@@ -118,10 +118,15 @@ __device__ inline void group_fwd(const FwdPtrs& t, const GroupItem& it, int hl,
       const int64_t i = (k * G + hl) * L + m;
       ok[m] = i < it.nv;
       vi[m] = REV ? it.v1 - i : it.v0 + i;
-      load_vec<IO, true, true, true>(t.g, vi[m], ok[m], it.P0, it.P1, 1.0f,
-                                     g[m], t.pend);
-      load_vec<IO, true, true, true>(t.x, vi[m], ok[m], it.P0, it.P1, 0.0f,
-                                     x[m], t.pend);
+      const char* const src[2] = {t.g, t.x};
+      const float ident[2] = {1.0f, 0.0f};
+      float gx[2][V];
+      load_vecs<IO, 2>(src, vi[m], ok[m], it.P0, it.P1, ident, gx, t.pend);
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        g[m][e] = gx[0][e];
+        x[m][e] = gx[1][e];
+      }
     }
     float A = 1.0f, X = 0.0f;
 #pragma unroll
@@ -173,13 +178,28 @@ __device__ inline void group_bwd(const BwdPtrs& t, const GroupItem& it, int hl,
       const int64_t i = (k * G + hl) * L + m;
       ok[m] = i < it.nv;
       vi[m] = RB ? it.v1 - i : it.v0 + i;
-      if (!DYC)
-        load_vec<IO, true, true, true>(t.dy, vi[m], ok[m], it.P0, it.P1, 0.0f,
-                                       dy[m], t.pend);
-      load_vec<IO, true, true, true>(t.g, vi[m], ok[m], it.P0, it.P1, 1.0f,
-                                     g[m], t.pend);
-      load_vec<IO, true, true, true>(t.h, vi[m], ok[m], it.P0, it.P1, 0.0f,
-                                     h[m], t.pend);
+      if (DYC) {
+        const char* const src[2] = {t.g, t.h};
+        const float ident[2] = {1.0f, 0.0f};
+        float gh[2][V];
+        load_vecs<IO, 2>(src, vi[m], ok[m], it.P0, it.P1, ident, gh, t.pend);
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          g[m][e] = gh[0][e];
+          h[m][e] = gh[1][e];
+        }
+      } else {
+        const char* const src[3] = {t.dy, t.g, t.h};
+        const float ident[3] = {0.0f, 1.0f, 0.0f};
+        float ygh[3][V];
+        load_vecs<IO, 3>(src, vi[m], ok[m], it.P0, it.P1, ident, ygh, t.pend);
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          dy[m][e] = ygh[0][e];
+          g[m][e] = ygh[1][e];
+          h[m][e] = ygh[2][e];
+        }
+      }
     }
     // (DYC: the row value fills dy after the loads are issued, so that its
     // own load does not hold them back)
