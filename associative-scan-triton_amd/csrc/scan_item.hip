@@ -7,8 +7,9 @@
 namespace asc {
 namespace {
 
-// Short items: a mean segment of at most 4 sub-tiles (fp32 backward: 3).  Their waves run the shallow-pipeline kernels, whose lower
-// register count admits more waves per SIMD (fp32 forward 93 -> 57 VGPRs,
+// Short items: a mean segment of at most 4 sub-tiles (fp32 backward: 3,
+// fp16/bf16 backward: 6).  Their waves run the shallow-pipeline kernels,
+// whose lower register count admits more waves per SIMD (fp32 forward 93 -> 57 VGPRs,
 // bf16 backward 125 -> 96).  Measured on MI355X, uniform segments of
 // C=1024 rows: bf16 1024 elements 4.9 / 5.6 -> 6.2 / 6.2 TB/s (fwd / bwd),
 // 512 elements 3.4 / 4.3 -> 4.3 / 5.0; fp32 600 elements 5.7 / 5.3 ->
@@ -19,9 +20,14 @@ namespace {
 // 1024: 29.8 against 31.0 us; ragged segments of 16-2048 elements: 122 against
 // 128 us); the backward is slower shallow at 4 (ragged 500-1500: 246 against
 // 242 us) and keeps 3.
+// fp16/bf16 backward: up to 6 sub-tiles (with the edge sub-tiles' loads
+// issued together, the shallow backward's extra waves pay off further:
+// ragged 1-5000 bf16 elements 279.9 -> 259.0 us, uniform 3000 93.7 -> 91.1;
+// cfg3, a mean of 7.2 sub-tiles, stays deep: 420.9 against 429.7 us
+// shallow, and so does the forward, 244.2 against 261.8).
 bool short_items(const Geometry& geo, int v, bool bwd) {
   const int64_t mean = geo.T / (geo.S > 0 ? geo.S : 1);
-  const int64_t subtiles = v != 4 ? 4 : (bwd ? 3 : 4);
+  const int64_t subtiles = v != 4 ? (bwd ? 6 : 4) : (bwd ? 3 : 4);
   return mean <= subtiles * static_cast<int64_t>(kWave) * v;
 }
 
