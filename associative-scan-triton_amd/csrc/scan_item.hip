@@ -19,7 +19,8 @@ namespace {
 // past 4 sub-tiles, and at 4 its registers cost occupancy for nothing (T =
 // 1024: 29.8 against 31.0 us; ragged segments of 16-2048 elements: 122 against
 // 128 us); the backward is slower shallow at 4 (ragged 500-1500: 246 against
-// 242 us) and keeps 3.
+// 242 us) and keeps 3 (shallow up to 5 with the edge loads issued together:
+// ragged 500-1500 263.5 against 248.9 us; forward up to 6: no gain).
 // fp16/bf16 backward: up to 6 sub-tiles (with the edge sub-tiles' loads
 // issued together, the shallow backward's extra waves pay off further:
 // ragged 1-5000 bf16 elements 279.9 -> 259.0 us, uniform 3000 93.7 -> 91.1;
