@@ -1111,13 +1111,15 @@ bool tree_bwd(const BwdParams& p, int dtype, int dirs, bool aln, bool dyc,
               void* ws, int64_t ws_bytes, void* stream, int& status,
               const uint32_t** fail);
 
-// scan_pair.hip: two items per wave (one per 32-lane half) for short
-// segments.  pair_use: the geometry's mean segment fits one step of a half
-// (32 vectors); pair_fwd / pair_bwd launch it (16-byte aligned tensors, no
-// gate product; arguments validated).
-bool pair_use(const Geometry& geo, int v);
-int pair_fwd(const FwdParams& p, int dtype, int dirs, void* stream);
-int pair_bwd(const BwdParams& p, int dtype, int dirs, bool dyc, void* stream);
+// scan_group.hip: two or four items per wave (one per group of 32 or 16
+// lanes) for short segments.  group_walk_use: the geometry's mean segment
+// fits one step of a half (32 vectors); group_walk_fwd / group_walk_bwd
+// launch it (16-byte aligned tensors, no gate product; arguments
+// validated).
+bool group_walk_use(const Geometry& geo, int v);
+int group_walk_fwd(const FwdParams& p, int dtype, int dirs, void* stream);
+int group_walk_bwd(const BwdParams& p, int dtype, int dirs, bool dyc,
+                   void* stream);
 
 // scan_chain.hip: chained chunks for segments aligned to the chunk size.
 // chain_bytes: its workspace (0 when the geometry cannot use it).

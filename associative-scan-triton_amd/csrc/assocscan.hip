@@ -19,8 +19,8 @@ constexpr int64_t kScratchBytes = int64_t(8) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 // Short segments: two items per wave (1) or one (0).
-#ifndef ASC_PAIR_WALK
-#define ASC_PAIR_WALK 1
+#ifndef ASC_GROUP_WALK
+#define ASC_GROUP_WALK 1
 #endif
 
 // Few-item problems: the tree walk (1) or the look-back walk (0).
@@ -146,8 +146,8 @@ int run_fwd(const void* const* g, const void* const* x, void* const* h,
   const int nw = wa || chained ? 0 : pick_walk(S, C, T, nbranch, v, false);
   if (nw)
     st = wg_fwd(p, nw, dtype, dirs, aln, stream);
-  else if (ASC_PAIR_WALK && aln && !wa && !chained && pair_use(p.geo, v))
-    st = pair_fwd(p, dtype, dirs, stream);
+  else if (ASC_GROUP_WALK && aln && !wa && !chained && group_walk_use(p.geo, v))
+    st = group_walk_fwd(p, dtype, dirs, stream);
   else
     st = item_fwd(p, dtype, dirs, aln, wa, stream);
   if (st || !chained) return st;
@@ -237,8 +237,8 @@ int run_bwd(const void* const* dy, const void* const* g, const void* const* h,
   const int nw = chained ? 0 : pick_walk(S, C, T, nbranch, v, true);
   if (nw)
     st = wg_bwd(p, nw, dtype, dirs, aln, dyc, stream);
-  else if (ASC_PAIR_WALK && aln && !chained && pair_use(p.geo, v))
-    st = pair_bwd(p, dtype, dirs, dyc, stream);
+  else if (ASC_GROUP_WALK && aln && !chained && group_walk_use(p.geo, v))
+    st = group_walk_bwd(p, dtype, dirs, dyc, stream);
   else
     st = item_bwd(p, dtype, dirs, aln, dyc, stream);
   if (st || !chained) return st;

@@ -397,11 +397,11 @@ int group_lanes(const Geometry& geo, int v) {
 // (T = 256 / 512 fp32, 512 / 1024 bf16 and ragged segments of those means)
 // ran at best even with one wave per item and lost up to 25% in the
 // backward (the halves of a pair wait for the longer item).
-bool pair_use(const Geometry& geo, int v) {
+bool group_walk_use(const Geometry& geo, int v) {
   return geo.T <= (geo.S > 0 ? geo.S : 1) * static_cast<int64_t>(32) * v;
 }
 
-int pair_fwd(const FwdParams& p, int dtype, int dirs, void* stream) {
+int group_walk_fwd(const FwdParams& p, int dtype, int dirs, void* stream) {
   const int G = group_lanes(p.geo, 16 / elem_size(dtype));
   const void* fn = nullptr;
   switch (dtype) {
@@ -414,7 +414,8 @@ int pair_fwd(const FwdParams& p, int dtype, int dirs, void* stream) {
   return launch(fn, walk_grid(p, groups, 1), 1, p, stream);
 }
 
-int pair_bwd(const BwdParams& p, int dtype, int dirs, bool dyc, void* stream) {
+int group_walk_bwd(const BwdParams& p, int dtype, int dirs, bool dyc,
+                   void* stream) {
   const int G = group_lanes(p.geo, 16 / elem_size(dtype));
   const void* fn = nullptr;
   switch (dtype) {

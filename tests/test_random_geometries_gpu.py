@@ -7,7 +7,7 @@ chained walk's chunk with and without an element off the grid, long
 segments), with and without the workspace, and runs the forward in both
 directions, the backward of each, the two-branch calls and the row-constant
 gradient; sampled rows are compared with the oracle.  The walk a case takes
-follows from its geometry (tree, chained with its one-wave partner, pair,
+follows from its geometry (tree, chained with its one-wave partner, group,
 one-wave, workgroup), so the draws cover their mixtures as well.
 """
 

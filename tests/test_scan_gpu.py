@@ -1183,8 +1183,9 @@ def no_workspace():
 @pytest.mark.parametrize("name", sorted(PAIR_LENS))
 @pytest.mark.parametrize("C", [7, 130])
 def test_pair_walk_parity(dtype, name, C, no_workspace):
-  """Forward (both directions) and dense backward (both) against the
-  oracle; an odd number of items leaves the last pair with one item."""
+  """The group walk (two or four short items per wave): forward (both
+  directions) and dense backward (both) against the oracle; an item count
+  that is not a multiple of the group count leaves the last wave short."""
   from associative_scan_triton import _ops
   lens = PAIR_LENS[name]
   _pair_geometry(lens, dtype)
@@ -1205,7 +1206,7 @@ def test_pair_walk_parity(dtype, name, C, no_workspace):
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("name", ["ragged", "odd", "ragged2", "quad-ragged"])
 def test_pair_walk_bidirectional_and_row_gradient(dtype, name, no_workspace):
-  """Both branches in one launch (each pair's two items from one branch),
+  """Both branches in one launch (each wave's items from one branch),
   and a gradient constant along time (each half reads its row's value):
   bits equal to the dense gradient's, values against the oracle."""
   from associative_scan_triton import _ops
