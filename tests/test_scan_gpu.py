@@ -1150,7 +1150,7 @@ def test_chain_walk_bidirectional(dtype, mixed):
 
 # (means of up to one step of a half, and a few geometries just past it,
 # which run one wave per item)
-PAIR_LENS = {
+GROUP_LENS = {
   "uniform": [128] * 8,
   # items of several steps of a half beside one-element and empty ones
   "ragged": [1, 300, 7, 0, 129, 64, 2, 33, 97],
@@ -1165,7 +1165,7 @@ PAIR_LENS = {
 }
 
 
-def _pair_geometry(lens, dtype):
+def _group_geometry(lens, dtype):
   per_half = 128 if dtype == torch.float32 else 256
   assert sum(lens) <= len(lens) * 4 * per_half
 
@@ -1180,15 +1180,15 @@ def no_workspace():
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
-@pytest.mark.parametrize("name", sorted(PAIR_LENS))
+@pytest.mark.parametrize("name", sorted(GROUP_LENS))
 @pytest.mark.parametrize("C", [7, 130])
-def test_pair_walk_parity(dtype, name, C, no_workspace):
+def test_group_walk_parity(dtype, name, C, no_workspace):
   """The group walk (two or four short items per wave): forward (both
   directions) and dense backward (both) against the oracle; an item count
   that is not a multiple of the group count leaves the last wave short."""
   from associative_scan_triton import _ops
-  lens = PAIR_LENS[name]
-  _pair_geometry(lens, dtype)
+  lens = GROUP_LENS[name]
+  _group_geometry(lens, dtype)
   g, x, dy = make(lens, C, dtype, glo=0.5, n=3)
   gd, xd, dyd = g.to(DEV), x.to(DEV), dy.to(DEV)
   cu = torch.tensor(cu_of(lens), device=DEV)
@@ -1205,13 +1205,13 @@ def test_pair_walk_parity(dtype, name, C, no_workspace):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("name", ["ragged", "odd", "ragged2", "quad-ragged"])
-def test_pair_walk_bidirectional_and_row_gradient(dtype, name, no_workspace):
+def test_group_walk_bidirectional_and_row_gradient(dtype, name, no_workspace):
   """Both branches in one launch (each wave's items from one branch),
   and a gradient constant along time (each half reads its row's value):
   bits equal to the dense gradient's, values against the oracle."""
   from associative_scan_triton import _ops
-  lens, C = PAIR_LENS[name], 9
-  _pair_geometry(lens, dtype)
+  lens, C = GROUP_LENS[name], 9
+  _group_geometry(lens, dtype)
   gf, xf, dyf = make(lens, C, dtype, seed=1, glo=0.5, n=3)
   gb, xb, dyb = make(lens, C, dtype, seed=2, glo=0.5, n=3)
   cu = torch.tensor(cu_of(lens), device=DEV)
