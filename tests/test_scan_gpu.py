@@ -305,8 +305,9 @@ def test_nonfinite_values_stay_in_their_segment(walk):
 @pytest.mark.parametrize("offsets", [(1, 1, 1), (2, 2, 2), (3, 1, 2), (0, 1, 0)],
                          ids=["phase1", "phase2", "mixed", "mixed2"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
-@pytest.mark.parametrize("lens", [[700, 1, 33, 1500], [40000, 3, 90001]],
-                         ids=["short", "long"])
+@pytest.mark.parametrize("lens", [[100, 1, 33, 150], [700, 1, 33, 1500],
+                                  [40000, 3, 90001]],
+                         ids=["tiny", "short", "long"])
 def test_misaligned_views(offsets, dtype, lens, walk):
   C = 3
   T = sum(lens)
