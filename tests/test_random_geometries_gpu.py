@@ -6,9 +6,12 @@ lengths around the 16-byte vector and the sub-tile, multiples of the
 chained walk's chunk with and without an element off the grid, long
 segments), with and without the workspace, and runs the forward in both
 directions, the backward of each, the two-branch calls and the row-constant
-gradient; sampled rows are compared with the oracle.  The walk a case takes
-follows from its geometry (tree, chained with its one-wave partner, group,
-one-wave, workgroup), so the draws cover their mixtures as well.
+gradient; sampled rows are compared with the oracle.  In 30% of the cases
+the single-branch tensors are views at independent element offsets 0-7
+(their phases on the 16-byte grid differ, as with sliced inputs).  The walk
+a case takes follows from its geometry (tree, look-back, chained with its
+one-wave partner, group, one-wave, workgroup), so the draws cover their
+mixtures as well.
 """
 
 from __future__ import annotations
@@ -23,7 +26,7 @@ from associative_scan_triton import _ops
 pytestmark = pytest.mark.gpu
 
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
-NCASES = 48
+NCASES = 96
 
 
 def _chunk(dtype):
@@ -34,12 +37,14 @@ def _draw(seed):
   rng = np.random.default_rng(seed)
   dtype = DTYPES[rng.integers(3)]
   CH = _chunk(dtype)
-  kind = rng.choice(["short", "mixed", "chunky", "long"])
+  kind = rng.choice(["short", "mixed", "chunky", "long", "tiny", "tiny"])
   S = int(rng.integers(1, 24))
   lens = []
   for _ in range(S):
     r = rng.random()
-    if kind == "short":
+    if kind == "tiny":
+      n = int(rng.integers(0, 140)) if r < 0.9 else int(rng.integers(140, 600))
+    elif kind == "short":
       n = int(rng.integers(0, 300)) if r < 0.9 else int(rng.integers(300, 2000))
     elif kind == "chunky":
       n = CH * int(rng.integers(1, 4)) + (int(rng.integers(-3, 4)) if r < 0.3 else 0)
@@ -57,32 +62,48 @@ def _draw(seed):
   return dtype, lens, C, use_ws
 
 
+def _place(t, off):
+  """t on the device; off >= 0: as a view that starts off elements into a
+  fresh buffer (a pointer off the 16-byte grid for off not a multiple of the
+  vector)."""
+  if off < 0:
+    return t.to(DEV)
+  buf = torch.zeros(t.numel() + 16, dtype=t.dtype, device=DEV)
+  v = buf[off:off + t.numel()].view(t.shape)
+  v.copy_(t.to(DEV))
+  return v
+
+
 @pytest.mark.parametrize("seed", range(NCASES))
 def test_random_geometry(seed):
   dtype, lens, C, use_ws = _draw(seed)
   T = sum(lens)
   g, x, dy = make(lens, C, dtype, seed=seed, glo=0.5, n=3)
-  gd, xd, dyd = g.to(DEV), x.to(DEV), dy.to(DEV)
+  orng = np.random.default_rng(seed + 77)
+  mis = bool(orng.random() < 0.3)
+  offs = [int(v) for v in orng.integers(0, 8, 6)] if mis else [-1] * 6
+  gd, xd, dyd = _place(g, offs[0]), _place(x, offs[1]), _place(dy, offs[2])
   cu = torch.tensor(cu_of(lens), device=DEV)
   rows = sorted({0, C // 2, C - 1})
   prev = _ops.USE_WORKSPACE
   _ops.USE_WORKSPACE = use_ws
   try:
     for rev in (False, True):
-      h = torch.empty_like(xd)
+      h = _place(torch.zeros_like(x), offs[3])
       _ops.scan_fwd(gd, xd, h, cu, reverse=rev)
-      dx, dg = torch.empty_like(xd), torch.empty_like(xd)
+      dx, dg = _place(torch.zeros_like(x), offs[4]), _place(torch.zeros_like(x), offs[5])
       _ops.scan_bwd(dyd, gd, h, dx, dg, cu, causal=not rev)
       torch.cuda.synchronize()
       for r in rows:
         sl = slice(r, r + 1)
-        what = f"seed {seed} {dtype} C={C} S={len(lens)} T={T} ws={use_ws} rev={rev} row {r}"
+        what = f"seed {seed} {dtype} C={C} S={len(lens)} T={T} ws={use_ws} rev={rev} offs={offs} row {r}"
         check_close(h[sl], oracle_fwd(g[sl], x[sl], lens, reverse=rev), dtype,
                     "h " + what)
         dx_ref, dg_ref = oracle_bwd(dy[sl], g[sl], npf(h[sl]), lens,
                                     causal=not rev)
         check_close(dx[sl], dx_ref, dtype, "dx " + what)
         check_close(dg[sl], dg_ref, dtype, "dg " + what)
+    gd, xd, dyd = g.to(DEV), x.to(DEV), dy.to(DEV)
     # both branches in one call, and the gradient of out.sum() (one value
     # per row) against the same gradient materialised
     hf, hb = torch.empty_like(xd), torch.empty_like(xd)
