@@ -130,3 +130,53 @@ def test_random_geometry(seed):
       check_close(outs[3][sl], dgb, dtype, "dgb " + what)
   finally:
     _ops.USE_WORKSPACE = prev
+
+
+@pytest.mark.parametrize("seed", range(1000, 1032))
+def test_random_recompute_geometry(seed):
+  """The recompute backward (asc_scan_bwd_recompute, whichever walk it takes)
+  on the same draws, one direction and a dense or row-constant gradient per
+  seed, against the oracle; rows a whole number of 16-byte vectors (its
+  contract), except every tenth seed, which must be refused."""
+  from associative_scan_triton._lib import AscError
+  from test_recompute_gpu import _chunk as _rc_chunk, _ckpt_expected, _stored
+  dtype, lens, C, use_ws = _draw(seed)
+  if seed % 10:
+    lens[-1] += (-sum(lens)) % (4 if dtype == torch.float32 else 8)
+  T = sum(lens)
+  g, x, dy = make(lens, C, dtype, seed=seed, glo=0.5, n=3)
+  gd, xd = g.to(DEV), x.to(DEV)
+  cu = torch.tensor(cu_of(lens), device=DEV)
+  rows = sorted({0, C // 2, C - 1})
+  rng = np.random.default_rng(seed + 5)
+  causal = bool(rng.random() < 0.5)
+  rowgrad = bool(rng.random() < 0.3)
+  if rowgrad:
+    dy = torch.randn(C, 1, generator=torch.Generator().manual_seed(seed)).to(
+      dtype).expand(C, T)
+    dyd = dy[:, :1].to(DEV).expand(C, T)
+  else:
+    dyd = dy.to(DEV)
+  h = torch.empty_like(xd)
+  _ops.scan_fwd(gd, xd, h, cu, reverse=not causal)
+  ck = _ops.scan_checkpoints(h, cu, reverse=not causal)
+  dx, dg = torch.empty_like(xd), torch.empty_like(xd)
+  prev = _ops.USE_WORKSPACE
+  _ops.USE_WORKSPACE = use_ws
+  try:
+    if T % (4 if dtype == torch.float32 else 8):
+      with pytest.raises(AscError, match="aligned"):
+        _ops.scan_bwd_recompute_kernel(dyd, gd, xd, ck, dx, dg, cu, causal)
+      return
+    _ops.scan_bwd_recompute_kernel(dyd, gd, xd, ck, dx, dg, cu, causal)
+    torch.cuda.synchronize()
+  finally:
+    _ops.USE_WORKSPACE = prev
+  what = (f"seed {seed} {dtype} C={C} S={len(lens)} T={T} ws={use_ws} "
+          f"causal={causal} rowgrad={rowgrad}")
+  h_st = _stored(oracle_fwd(g[rows], x[rows], lens, reverse=not causal), dtype)
+  dx_ref, dg_ref = oracle_bwd(dy[rows], g[rows], h_st, lens, causal=causal)
+  check_close(dx[rows], dx_ref, dtype, "dx " + what)
+  check_close(dg[rows], dg_ref, dtype, "dg " + what)
+  exp = _ckpt_expected(npf(h[rows]), lens, not causal, _rc_chunk(dtype))
+  assert np.array_equal(npf(ck[rows]), exp), "checkpoints " + what
