@@ -180,3 +180,44 @@ def test_random_recompute_geometry(seed):
   check_close(dg[rows], dg_ref, dtype, "dg " + what)
   exp = _ckpt_expected(npf(h[rows]), lens, not causal, _rc_chunk(dtype))
   assert np.array_equal(npf(ck[rows]), exp), "checkpoints " + what
+
+
+@pytest.mark.parametrize("seed", range(2000, 2032))
+def test_random_shift_pad_geometry(seed):
+  """shift_pad on the same draws (empty segments made one element long),
+  contiguous, at element offsets or transposed (strides (1, C)), either edge
+  rule, int32 or int64 cu_seqlens, against the oracle bit for bit; nothing
+  outside an offset output view is written."""
+  from oracle import oracle
+  dtype, lens, C, _ = _draw(seed)
+  lens = [max(n, 1) for n in lens]
+  L = sum(lens)
+  C = min(C, max(1, 2_000_000 // L))
+  rng = np.random.default_rng(seed + 11)
+  backward, wrap = bool(rng.random() < 0.5), bool(rng.random() < 0.5)
+  pad = float(rng.choice([0.0, 1.0, -2.5]))
+  layout = rng.choice(["contig", "offset", "transposed"])
+  data = torch.randn(C, L, generator=torch.Generator().manual_seed(seed)).to(dtype)
+  cu_np = cu_of(lens)
+  cu = torch.tensor(cu_np, device=DEV,
+                    dtype=torch.int32 if rng.random() < 0.5 else torch.int64)
+  oo = 0
+  if layout == "offset":
+    od, oo = int(rng.integers(0, 8)), int(rng.integers(0, 8))
+    dbuf = torch.zeros(C * L + 8, dtype=dtype, device=DEV)
+    obuf = torch.full((C * L + 8,), 7.0, dtype=dtype, device=DEV)
+    dv = dbuf[od:od + C * L].view(C, L)
+    dv.copy_(data.to(DEV))
+    ov = obuf[oo:oo + C * L].view(C, L)
+  elif layout == "transposed":
+    dv = data.t().contiguous().to(DEV).t()
+    ov = torch.empty(L, C, dtype=dtype, device=DEV).t()
+  else:
+    dv = data.to(DEV)
+    ov = torch.empty_like(dv)
+  _ops.shift_pad(dv, ov, cu, pad, backward=backward, wrap=wrap)
+  ref = oracle.shift_pad(npf(data), cu_np, pad, backward, wrap=wrap)
+  assert torch.equal(ov.cpu(), torch.from_numpy(ref).to(dtype)), (
+    f"seed {seed} {dtype} C={C} L={L} {layout} backward={backward} wrap={wrap}")
+  if layout == "offset":
+    assert torch.all(obuf[:oo] == 7.0) and torch.all(obuf[oo + C * L:] == 7.0)
