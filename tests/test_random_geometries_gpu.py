@@ -221,3 +221,66 @@ def test_random_shift_pad_geometry(seed):
     f"seed {seed} {dtype} C={C} L={L} {layout} backward={backward} wrap={wrap}")
   if layout == "offset":
     assert torch.all(obuf[:oo] == 7.0) and torch.all(obuf[oo + C * L:] == 7.0)
+
+
+@pytest.mark.parametrize("seed", range(3000, 3024))
+def test_random_public_api(seed):
+  """The public autograd functions (eager and compiled, causal and
+  bidirectional, with and without recompute_states) on the same draws, with
+  a loss of out.sum(), row-weighted sums or a dense gradient, against the
+  oracle on sampled rows."""
+  import associative_scan_triton as ast
+  from _helpers import grid_args
+  dtype, lens, C, _ = _draw(seed)
+  T = sum(lens)
+  rng = np.random.default_rng(seed + 3)
+  bidi = bool(rng.random() < 0.4)
+  compiled = bool(rng.random() < 0.5)
+  rec = bool(rng.random() < 0.3)
+  loss = rng.choice(["sum", "rowweights", "dense"])
+  g, x, x2 = make(lens, C, dtype, seed=seed, glo=0.5, n=3)
+  g2 = g.clone()
+  args = grid_args(lens, C, cu_dtype=torch.int64 if rng.random() < 0.5 else torch.int32)
+  w = torch.rand(C, generator=torch.Generator().manual_seed(seed)).to(dtype)
+  dense = torch.randn(C, T, generator=torch.Generator().manual_seed(seed + 1)).to(dtype)
+  def grad_of(y):
+    if loss == "sum":
+      return torch.ones(C, T, dtype=dtype)
+    if loss == "rowweights":
+      return w[:, None].expand(C, T).contiguous()
+    return dense
+  def back(y):
+    if loss == "sum":
+      return y.sum()
+    if loss == "rowweights":
+      return (y.sum(-1) * w.to(DEV)).sum()
+    return (y * dense.to(DEV)).sum()
+  tens = [t.to(DEV).requires_grad_(True) for t in ((g, x, g2, x2) if bidi else (g, x))]
+  rows = sorted({0, C // 2, C - 1})
+  what = f"seed {seed} {dtype} C={C} S={len(lens)} T={T} bidi={bidi} compiled={compiled} rec={rec} loss={loss}"
+  if bidi:
+    fn = ast.scan_bidirectional_branched_compiled if compiled else ast.scan_bidirectional_branched
+    yf, yb = fn(*tens, args, recompute_states=rec)
+    (back(yf) + back(yb)).backward()
+    dyf = grad_of(yf)
+    for r in rows:
+      sl = slice(r, r + 1)
+      check_close(yf.detach()[sl], oracle_fwd(g[sl], x[sl], lens), dtype, "yf " + what)
+      check_close(yb.detach()[sl], oracle_fwd(g2[sl], x2[sl], lens, reverse=True), dtype, "yb " + what)
+      dxr, dgr = oracle_bwd(dyf[sl], g[sl], npf(yf.detach()[sl]), lens, causal=True)
+      check_close(tens[1].grad[sl], dxr, dtype, "dxf " + what)
+      check_close(tens[0].grad[sl], dgr, dtype, "dgf " + what)
+      dxr, dgr = oracle_bwd(dyf[sl], g2[sl], npf(yb.detach()[sl]), lens, causal=False)
+      check_close(tens[3].grad[sl], dxr, dtype, "dxb " + what)
+      check_close(tens[2].grad[sl], dgr, dtype, "dgb " + what)
+  else:
+    fn = ast.scan_causal_compiled if compiled else ast.scan_causal
+    y = fn(*tens, args, recompute_states=rec)
+    back(y).backward()
+    dy = grad_of(y)
+    for r in rows:
+      sl = slice(r, r + 1)
+      check_close(y.detach()[sl], oracle_fwd(g[sl], x[sl], lens), dtype, "y " + what)
+      dxr, dgr = oracle_bwd(dy[sl], g[sl], npf(y.detach()[sl]), lens, causal=True)
+      check_close(tens[1].grad[sl], dxr, dtype, "dx " + what)
+      check_close(tens[0].grad[sl], dgr, dtype, "dg " + what)
