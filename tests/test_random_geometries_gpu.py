@@ -8,7 +8,8 @@ segments), with and without the workspace, and runs the forward in both
 directions, the backward of each, the two-branch calls and the row-constant
 gradient; sampled rows are compared with the oracle.  In 30% of the cases
 the single-branch tensors are views at independent element offsets 0-7
-(their phases on the 16-byte grid differ, as with sliced inputs).  The walk
+(their phases on the 16-byte grid differ, as with sliced inputs), and so
+are the two-branch tensors.  The walk
 a case takes follows from its geometry (tree, look-back, chained with its
 one-wave partner, group, one-wave, workgroup), so the draws cover their
 mixtures as well.
@@ -103,19 +104,28 @@ def test_random_geometry(seed):
                                     causal=not rev)
         check_close(dx[sl], dx_ref, dtype, "dx " + what)
         check_close(dg[sl], dg_ref, dtype, "dg " + what)
-    gd, xd, dyd = g.to(DEV), x.to(DEV), dy.to(DEV)
+    bo = [int(v) for v in orng.integers(0, 8, 9)] if mis else [-1] * 9
+    gd, xd, dyd = _place(g, bo[0]), _place(x, bo[1]), _place(dy, bo[2])
     # both branches in one call, and the gradient of out.sum() (one value
     # per row) against the same gradient materialised
-    hf, hb = torch.empty_like(xd), torch.empty_like(xd)
+    hf, hb = _place(torch.zeros_like(x), bo[3]), _place(torch.zeros_like(x), bo[4])
     _ops.scan_bidi_fwd(gd, xd, gd, dyd, hf, hb, cu)
-    outs = [torch.empty_like(xd) for _ in range(4)]
+    outs = [_place(torch.zeros_like(x), bo[5 + i]) for i in range(4)]
     _ops.scan_bidi_bwd(dyd, xd, gd, gd, hf, hb, *outs, cu)
     ones = torch.ones(C, dtype=dtype, device=DEV)
     dx1, dg1, dx2, dg2 = (torch.empty_like(xd) for _ in range(4))
     _ops.scan_bwd_rowgrad(ones, 1, gd, hf, dx1, dg1, cu, True)
     _ops.scan_bwd(torch.ones_like(xd), gd, hf, dx2, dg2, cu, causal=True)
     torch.cuda.synchronize()
-    assert torch.equal(dx1, dx2) and torch.equal(dg1, dg2), f"seed {seed}"
+    if mis:
+      # tensors of different phases may take the look-back walk, whose last
+      # bits can differ between two calls
+      tol = 1e-5 if dtype == torch.float32 else 1e-2
+      for a, b in ((dx1, dx2), (dg1, dg2)):
+        sc = max(1.0, float(b.float().abs().mean()))
+        torch.testing.assert_close(a.float(), b.float(), rtol=tol, atol=tol * sc)
+    else:
+      assert torch.equal(dx1, dx2) and torch.equal(dg1, dg2), f"seed {seed}"
     for r in rows:
       sl = slice(r, r + 1)
       what = f"seed {seed} two-branch row {r}"
